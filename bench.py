@@ -1,0 +1,248 @@
+#!/usr/bin/env python
+"""Benchmark: ring-attention block fwd+bwd on one MI355X.
+
+Metric: ring-attn fwd+bwd TFLOP/s and % of bf16 MFMA peak at
+S_local=8192, D=128 — config 4: B=1, H=24, D=128, T=8192 local queries, KV
+streamed as 8 chunks of 8192 (8 ring steps, 65536 keys), bf16 N(0,1) inputs
+from seed 3407, non-causal.
+
+One step = the hot path once: ring_attention_forward (V panel pack + fused
+forward kernel), ring_attention_delta (D = rowsum(dO*O)), and
+ring_attention_backward (K/Q/dO panel packs + dK/dV kernel + dQ kernel),
+called through torch.ops.ring_attention_ops with every input and output
+resident in HBM.  FLOP_total = 14*B*H*T*L*D (fwd 4, bwd 10; L = valid keys).
+
+Prints ONE JSON line.  --gpus N with N > 1 is refused: this build measures one
+GPU (multi-GPU sharding is a design, not a measured path).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+PEAK_BF16_TFLOPS = 2516.6  # 256 CU x 2.4 GHz x 4096 FLOP/clk/CU (dense)
+PEAK_HBM_GBS = 8000.0
+
+CONFIGS = {
+    1: dict(B=1, H=8, T=512, D=64, N=1, tc=512, lens=None, vscale=1.0),
+    2: dict(B=1, H=16, T=2048, D=64, N=4, tc=2048, lens=None, vscale=1.0),
+    3: dict(B=2, H=16, T=4096, D=72, N=8, tc=4096, lens=None, vscale=0.5),
+    4: dict(B=1, H=24, T=8192, D=128, N=8, tc=8192, lens=None, vscale=1.0),
+    5: dict(B=1, H=24, T=4429, D=128, N=4, tc=4480, lens=[4429] * 4, vscale=1.0),
+}
+
+
+def make_inputs_dev(cfg, seed, device):
+    """Seeded inputs (draw order Q, K chunks, V chunks, dO; fp32 randn -> bf16)
+    laid out token-major on the device; k/v hold all chunks along T."""
+    import torch
+
+    B, H, T, D, N, tc = cfg["B"], cfg["H"], cfg["T"], cfg["D"], cfg["N"], cfg["tc"]
+    g = torch.Generator().manual_seed(seed)
+
+    def draw(rows):
+        x = torch.randn((B, rows, H, D), generator=g, dtype=torch.float32)
+        if cfg["vscale"] != 1.0:
+            x = x * cfg["vscale"]
+        return x.to(torch.bfloat16)
+
+    q = draw(T).to(device).transpose(1, 2)
+    k = torch.empty((B, N * tc, H, D), dtype=torch.bfloat16, device=device)
+    v = torch.empty_like(k)
+    for c in range(N):
+        k[:, c * tc:(c + 1) * tc] = draw(tc).to(device)
+    for c in range(N):
+        v[:, c * tc:(c + 1) * tc] = draw(tc).to(device)
+    do = draw(T).to(device).transpose(1, 2)
+    return q, k.transpose(1, 2), v.transpose(1, 2), do
+
+
+def cpu_threads() -> int:
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count() or 1
+    cap = os.environ.get("OMP_NUM_THREADS")
+    if cap and cap.isdigit():
+        n = min(n, int(cap))
+    return max(1, n)
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(cfg, target_s: float):
+    """The reference algorithm as PyTorch CPU ops (oracle.cpu_baseline_fwd_bwd)
+    on a bounded sample of the workload: one head, a subset of query rows,
+    the full KV length.  Returns the cpu_baseline JSON object."""
+    import torch
+
+    from oracle import ring_attn_oracle as orc
+
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    B, D, N, T, tc = 1, cfg["D"], cfg["N"], cfg["T"], cfg["tc"]
+    lens = cfg["lens"] or [tc] * N
+    L = sum(lens)
+    scale = 1.0 / math.sqrt(D)
+
+    def run(tq):
+        q, ks, vs, do = orc.make_inputs(B, 1, tq, D, N, seed=1, chunk_len=tc, value_scale=cfg["vscale"])
+        ks = [k[:, :, :n] for k, n in zip(ks, lens)]
+        vs = [v[:, :, :n] for v, n in zip(vs, lens)]
+        t0 = time.perf_counter()
+        orc.cpu_baseline_fwd_bwd(q, ks, vs, do, scale)
+        return time.perf_counter() - t0
+
+    run(64)  # warm up oneDNN / thread pool
+    tq = 128
+    dt = run(tq)
+    tq_target = int(min(T, max(128, tq * target_s / max(dt, 1e-3))) // 128 * 128)
+    tq = max(128, tq_target)
+    dt = run(tq)
+    flops = 14.0 * 1 * 1 * tq * L * D
+    return {
+        "value": round(flops / dt / 1e12, 4),
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"1 of {cfg['H']} heads x {tq} of {T} query rows against all {L} keys "
+                   f"({N} chunks), fwd+bwd, {dt:.1f} s on {cpu_model()}"),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", type=int, default=4, choices=sorted(CONFIGS))
+    ap.add_argument("--seed", type=int, default=3407)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU-baseline sample time")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: --gpus {args.gpus} is not supported; this build measures the ring-attention "
+              "block on exactly one GPU (all ring steps of one rank's share on that GPU).", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import harp_amd
+    from harp_amd import _lib
+
+    assert torch.cuda.is_available(), "bench.py needs a HIP device"
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    harp_amd.load_ops()
+    ops = torch.ops.ring_attention_ops
+
+    cfg = CONFIGS[args.config]
+    B, H, T, D, N, tc = cfg["B"], cfg["H"], cfg["T"], cfg["D"], cfg["N"], cfg["tc"]
+    lens = cfg["lens"]
+    L = sum(lens) if lens else N * tc
+    scale = 1.0 / math.sqrt(D)
+    q, k, v, do = make_inputs_dev(cfg, args.seed, dev)
+    out = torch.empty((B, T, H, D), device=dev, dtype=torch.float32).transpose(1, 2)
+    m_i = torch.empty((B, H, T, 1), device=dev, dtype=torch.bfloat16)
+    l_i = torch.empty((B, H, T, 1), device=dev, dtype=torch.float32)
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(k)
+    dv = torch.empty_like(v)
+
+    def step():
+        ops.ring_attention_forward(q, k, v, out, m_i, l_i, N, scale, 0, lens)
+        delta = ops.ring_attention_delta(do, out)
+        ops.ring_attention_backward(q, dq, k, dk, v, dv, do, m_i, l_i, delta, N, scale, 0, lens)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    _lib.timing_read()  # discard
+    _lib.timing_enable(True)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    wall_s = time.perf_counter() - t_wall
+    _lib.timing_enable(False)
+    kt = _lib.timing_read()
+    ms_per_step = e0.elapsed_time(e1) / args.steps
+
+    bhtld = float(B) * H * T * L * D
+    flop_total = 14.0 * bhtld
+    tflops = flop_total / (ms_per_step * 1e-3) / 1e12
+    # algorithmic MFMA work per launch in this design's accounting
+    kernel_flops = {"fwd": 4.0 * bhtld, "dkdv": 8.0 * bhtld, "dq": 2.0 * bhtld}
+    kernels = {}
+    for name, (ms, n) in kt.items():
+        if n:
+            avg = ms / n
+            entry = {"avg_ms": round(avg, 4), "launches_per_step": n / args.steps}
+            if name in kernel_flops:
+                entry["tflops_algorithmic"] = round(kernel_flops[name] / (avg * 1e-3) / 1e12, 1)
+            kernels[name] = entry
+    dom = max((n for n in kernel_flops if n in kernels), key=lambda n: kt[n][0])
+    dom_tf = kernels[dom]["tflops_algorithmic"]
+    fwd_ms = kt["fwd"][0] / args.steps
+    bwd_ms = (kt["dkdv"][0] + kt["dq"][0] + kt["delta"][0]) / args.steps
+
+    result = {
+        "metric": "ring-attn fwd+bwd TFLOP/s and % bf16 MFMA peak, S_local=8192 D=128",
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) bf16, draw order Q, K chunks, V chunks, dO)",
+        "config": {
+            "workload": f"BASELINE config {args.config}: ring attention fwd+bwd, one rank's share on one GPU",
+            "B": B, "H": H, "D": D, "S_local": T, "kv_chunks": N, "chunk_len": tc, "L_valid": L,
+            "causal": False, "parallelism": "single GPU, ring steps streamed from HBM",
+        },
+        "pct_bf16_peak": round(100.0 * tflops / PEAK_BF16_TFLOPS, 2),
+        "fwd_ms": round(fwd_ms, 4),
+        "bwd_ms": round(bwd_ms, 4),
+        "kernels": kernels,
+        "wall_s_timed": round(wall_s, 3),
+        "roofline": {
+            "bound": "mfma",
+            "kernel": dom,
+            "achieved": dom_tf,
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(dom_tf / PEAK_BF16_TFLOPS, 4),
+            "traffic": None,
+        },
+        "cpu_baseline": None,
+        "gpu": torch.cuda.get_device_name(0),
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,22 @@
+"""harp_amd — MI355X (gfx950) ring-attention block for HARP's sequence-parallel attention.
+
+Drop-in for HARP's ``libring_attention_ops.so`` (namespace ``ring_attention_ops``):
+hand-written HIP kernels behind the C ABI of ``include/harp_ring_attn.h``
+(``kernels/libharp_ra.so``) and a PyTorch-ROCm operator library
+(``kernels/libring_attention_ops.so``).  Build with ``python -m harp_amd.build``.
+"""
+
+from ._lib import ABI_LIB, OPS_LIB, load_abi, load_ops  # noqa: F401
+from .ops import (  # noqa: F401
+    RingAttention,
+    abi_backward,
+    abi_delta,
+    abi_forward,
+    backward_workspace_bytes,
+    concat_chunks,
+    forward_workspace_bytes,
+    ring_attention,
+)
+from .wait_engine import CommWork, WaitEngine  # noqa: F401
+
+__version__ = "0.1.0"

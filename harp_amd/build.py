@@ -1,0 +1,134 @@
+"""Build the gfx950 libraries in-tree (no JIT cache, no setuptools).
+
+Outputs (both under ``kernels/`` at the repository root, next to each other
+so the operator library finds the C-ABI library through ``$ORIGIN``):
+
+* ``libharp_ra.so``              HIP kernels + the C ABI of include/harp_ring_attn.h
+                                 (hipcc, --offload-arch=gfx950).
+* ``libring_attention_ops.so``   the PyTorch operator library (namespace
+                                 ``ring_attention_ops``), the drop-in for the
+                                 reference's kernels/libring_attention_ops.so
+                                 (gemm/ring_attention/Makefile:9-12, 36-37).
+
+Run ``python -m harp_amd.build`` (or ``__graft_entry__.build()``).
+"""
+
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent.parent
+CSRC = ROOT / "harp_amd" / "csrc"
+INCLUDE = ROOT / "include"
+OUT = ROOT / "kernels"
+ABI_LIB = OUT / "libharp_ra.so"
+OPS_LIB = OUT / "libring_attention_ops.so"
+
+HIP_SOURCES = ["ra_kernels.hip", "ra_abi.hip"]
+HIP_HEADERS = ["ra_common.h", "ra_kernels.h"]
+OPS_SOURCE = "torch_ring_attention_ops.cpp"
+
+ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+OFFLOAD_ARCH = "gfx950"
+
+HIPCC_FLAGS = [
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    "-fvisibility=hidden",
+    f"--offload-arch={OFFLOAD_ARCH}",
+    # packed-fp32 VALU ops are kept out of every gfx950 code object
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+    "-Wno-unused-command-line-argument",
+]
+
+
+def _run(cmd: list[str], verbose: bool) -> None:
+    if verbose:
+        print("+", " ".join(cmd), flush=True)
+    res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(
+        ln for ln in res.stdout.splitlines() if "packed-fp32-ops" not in ln and ln.strip()
+    )
+    if res.returncode != 0:
+        raise RuntimeError(f"build step failed ({res.returncode}): {' '.join(cmd)}\n{out}")
+    if verbose and out:
+        print(out)
+
+
+def build_abi(verbose: bool = False) -> Path:
+    OUT.mkdir(parents=True, exist_ok=True)
+    tmp = ABI_LIB.with_suffix(".so.tmp")
+    cmd = [str(ROCM / "bin" / "hipcc"), *HIPCC_FLAGS, f"-I{INCLUDE}"]
+    cmd += [str(CSRC / s) for s in HIP_SOURCES]
+    cmd += ["-o", str(tmp)]
+    _run(cmd, verbose)
+    os.replace(tmp, ABI_LIB)
+    return ABI_LIB
+
+
+def build_ops(verbose: bool = False) -> Path:
+    import torch.utils.cpp_extension as ce
+
+    OUT.mkdir(parents=True, exist_ok=True)
+    torch_lib = Path(ce.library_paths()[0])
+    incs = ce.include_paths()
+    tmp = OPS_LIB.with_suffix(".so.tmp")
+    abi = int(__import__("torch")._C._GLIBCXX_USE_CXX11_ABI)
+    cmd = [
+        "g++",
+        "-O2",
+        "-std=c++17",
+        "-fPIC",
+        "-shared",
+        "-D__HIP_PLATFORM_AMD__=1",
+        "-DUSE_ROCM=1",
+        f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+        "-DTORCH_EXTENSION_NAME=ring_attention_ops",
+        *[f"-I{p}" for p in incs],
+        f"-I{ROCM / 'include'}",
+        f"-I{INCLUDE}",
+        str(CSRC / OPS_SOURCE),
+        f"-L{OUT}",
+        "-lharp_ra",
+        f"-L{torch_lib}",
+        "-lc10",
+        "-lc10_hip",
+        "-ltorch_cpu",
+        "-ltorch",
+        "-Wl,-rpath,$ORIGIN",
+        f"-Wl,-rpath,{torch_lib}",
+        "-o",
+        str(tmp),
+    ]
+    _run(cmd, verbose)
+    os.replace(tmp, OPS_LIB)
+    return OPS_LIB
+
+
+def build(verbose: bool = False) -> None:
+    """Compile both libraries unconditionally (the build check)."""
+    build_abi(verbose)
+    build_ops(verbose)
+
+
+def sources_newer_than_libs() -> bool:
+    """True when a source file is newer than a built library (or one is missing)."""
+    libs = [ABI_LIB, OPS_LIB]
+    if not all(p.exists() for p in libs):
+        return True
+    newest_lib = min(p.stat().st_mtime for p in libs)
+    srcs = [CSRC / s for s in HIP_SOURCES + HIP_HEADERS + [OPS_SOURCE]] + [INCLUDE / "harp_ring_attn.h"]
+    return any(s.stat().st_mtime > newest_lib for s in srcs)
+
+
+if __name__ == "__main__":
+    build(verbose="-v" in sys.argv)
+    print(f"built {ABI_LIB} and {OPS_LIB}")

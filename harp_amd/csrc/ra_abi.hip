@@ -1,0 +1,500 @@
+// C ABI of libharp_ra.so: argument validation, workspace carving and kernel
+// sequencing for the ring-attention block.  See include/harp_ring_attn.h.
+//
+// Host flow mirrors the reference's operator bodies:
+//   forward  (ring_attn.cpp:2412-2575): pack V panels (:2452-2485) -> ring loop
+//            over all chunks (:2488-2568) -> O /= l (:2569-2573), here one
+//            pack launch + one fused kernel launch.
+//   backward (ring_attn.cpp:2577-2829): pack Q/dO/K panels (:2664-2717) ->
+//            per-chunk S/dP recompute, dQ/dK/dV (:2723-2816) -> dQ owner sum
+//            (:2817-2828), here pack launches + a dK/dV kernel and a dQ kernel
+//            whose fp32 register accumulators replace the dQ slot reduction.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/harp_ring_attn.h"
+#include "ra_kernels.h"
+
+using namespace harp_ra;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int ok() {
+  g_last_error.clear();
+  return HARP_RA_OK;
+}
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+int round64(int x) { return (x + 63) / 64 * 64; }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// bf16 operand that is read with 16-byte vector loads
+int check_bf16_view(const void* p, const int64_t* s, const char* name) {
+  if (!p) return fail(HARP_RA_EINVAL, "%s is NULL", name);
+  if (!s) return fail(HARP_RA_EINVAL, "%s strides are NULL", name);
+  if (!aligned16(p)) return fail(HARP_RA_EINVAL, "%s must be 16-byte aligned", name);
+  if (s[3] != 1) return fail(HARP_RA_EINVAL, "%s must have unit stride in D (got %lld)", name, (long long)s[3]);
+  for (int i = 0; i < 3; ++i)
+    if (s[i] < 0 || s[i] % 8 != 0)
+      return fail(HARP_RA_EINVAL, "%s stride[%d]=%lld must be a non-negative multiple of 8 elements", name, i,
+                  (long long)s[i]);
+  return HARP_RA_OK;
+}
+
+// scalar-stored / scalar-read operand
+int check_plain_view(const void* p, const int64_t* s, const char* name) {
+  if (!p) return fail(HARP_RA_EINVAL, "%s is NULL", name);
+  if (!s) return fail(HARP_RA_EINVAL, "%s strides are NULL", name);
+  if (s[3] != 1) return fail(HARP_RA_EINVAL, "%s must have unit stride in D (got %lld)", name, (long long)s[3]);
+  for (int i = 0; i < 3; ++i)
+    if (s[i] < 0) return fail(HARP_RA_EINVAL, "%s stride[%d] must be non-negative", name, i);
+  return HARP_RA_OK;
+}
+
+int check_dims(int batch, int h_num, int t_num, int h_len) {
+  if (batch < 1 || h_num < 1 || t_num < 1 || h_len < 1)
+    return fail(HARP_RA_EINVAL, "sizes must be positive (B=%d H=%d T=%d D=%d)", batch, h_num, t_num, h_len);
+  if (h_len % 8 != 0) return fail(HARP_RA_EUNSUPPORTED, "head dim D=%d must be a multiple of 8", h_len);
+  if (h_len > 128) return fail(HARP_RA_EUNSUPPORTED, "head dim D=%d > 128 is not supported", h_len);
+  if (batch > 65535 || h_num > 65535) return fail(HARP_RA_EUNSUPPORTED, "B and H must be <= 65535");
+  return HARP_RA_OK;
+}
+
+// Chunk geometry shared by forward/backward/workspace sizing.
+struct Geometry {
+  int n = 0;
+  int len[kMaxChunks] = {};
+  int off[kMaxChunks] = {};
+  int lp = 0;
+};
+
+int make_geometry(int sp_size, int kv_chunk_len, const int32_t* kv_valid_lens, Geometry* g) {
+  if (sp_size < 1 || sp_size > HARP_RA_MAX_CHUNKS)
+    return fail(HARP_RA_EINVAL, "sp_size=%d must be in [1, %d]", sp_size, HARP_RA_MAX_CHUNKS);
+  if (kv_chunk_len < 1) return fail(HARP_RA_EINVAL, "kv_chunk_len=%d must be positive", kv_chunk_len);
+  g->n = sp_size;
+  int64_t lp = 0;
+  for (int c = 0; c < sp_size; ++c) {
+    const int len = kv_valid_lens ? kv_valid_lens[c] : kv_chunk_len;
+    if (len < 0 || len > kv_chunk_len)
+      return fail(HARP_RA_EINVAL, "kv_valid_lens[%d]=%d must be in [0, kv_chunk_len=%d]", c, len, kv_chunk_len);
+    g->len[c] = len;
+    g->off[c] = (int)lp;
+    lp += round64(len);
+  }
+  if (lp == 0) lp = 64;  // keep panels non-empty
+  if (lp > (int64_t)1 << 30) return fail(HARP_RA_EUNSUPPORTED, "total KV length too large");
+  g->lp = (int)lp;
+  return HARP_RA_OK;
+}
+
+size_t fwd_ws(int batch, int h_num, int h_len, const Geometry& g) {
+  return align_up((size_t)batch * h_num * padded_d(h_len) * g.lp * 2);
+}
+size_t bwd_ws(int batch, int h_num, int t_num, int h_len, const Geometry& g) {
+  const size_t dp = padded_d(h_len);
+  const size_t kt = align_up((size_t)batch * h_num * dp * g.lp * 2);
+  const size_t qt = align_up((size_t)batch * h_num * dp * round64(t_num) * 2);
+  return kt + 2 * qt;
+}
+
+// Library-owned grow-only workspace, one per device (used when the caller
+// passes workspace == NULL).
+struct OwnedWorkspace {
+  std::mutex mu;
+  void* ptr[64] = {};
+  size_t bytes[64] = {};
+};
+OwnedWorkspace& owned() {
+  static OwnedWorkspace w;
+  return w;
+}
+
+int resolve_workspace(void** ws, size_t* ws_bytes, size_t need) {
+  if (*ws) {
+    if (*ws_bytes < need)
+      return fail(HARP_RA_ENOMEM, "workspace of %zu bytes is smaller than the %zu bytes needed", *ws_bytes, need);
+    if ((reinterpret_cast<uintptr_t>(*ws) & 255u) != 0) return fail(HARP_RA_EINVAL, "workspace must be 256-byte aligned");
+    return HARP_RA_OK;
+  }
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return fail(HARP_RA_ELAUNCH, "hipGetDevice failed");
+  OwnedWorkspace& w = owned();
+  std::lock_guard<std::mutex> lock(w.mu);
+  if (w.bytes[dev] < need) {
+    if (w.ptr[dev]) {
+      // earlier calls may still use the old buffer on any stream
+      if (hipDeviceSynchronize() != hipSuccess) return fail(HARP_RA_ELAUNCH, "hipDeviceSynchronize failed");
+      (void)hipFree(w.ptr[dev]);
+      w.ptr[dev] = nullptr;
+      w.bytes[dev] = 0;
+    }
+    const size_t grow = need + need / 4;  // grow-only with headroom, like the reference's x1.25 slots
+    if (hipMalloc(&w.ptr[dev], grow) != hipSuccess) {
+      w.ptr[dev] = nullptr;
+      return fail(HARP_RA_ENOMEM, "hipMalloc of %zu workspace bytes failed", grow);
+    }
+    w.bytes[dev] = grow;
+  }
+  *ws = w.ptr[dev];
+  *ws_bytes = w.bytes[dev];
+  return HARP_RA_OK;
+}
+
+// Optional per-kernel event timing (harp_ra_timing_enable / _read).
+struct Timing {
+  bool on = false;
+  struct Rec {
+    int kind;
+    hipEvent_t a, b;
+  };
+  std::vector<Rec> recs;
+  std::vector<hipEvent_t> pool;
+  hipEvent_t get() {
+    if (!pool.empty()) {
+      hipEvent_t e = pool.back();
+      pool.pop_back();
+      return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+  }
+};
+Timing& timing() {
+  static Timing t;
+  return t;
+}
+
+// Brackets one kernel launch with timing events when timing is enabled.
+struct TimedLaunch {
+  int kind;
+  hipStream_t st;
+  hipEvent_t a = nullptr, b = nullptr;
+  TimedLaunch(int k, hipStream_t s) : kind(k), st(s) {
+    Timing& t = timing();
+    if (!t.on) return;
+    a = t.get();
+    b = t.get();
+    if (a && b) (void)hipEventRecord(a, st);
+  }
+  ~TimedLaunch() {
+    if (!a || !b) return;
+    (void)hipEventRecord(b, st);
+    timing().recs.push_back({kind, a, b});
+  }
+};
+
+int launched(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(HARP_RA_ELAUNCH, "%s launch failed: %s", what, hipGetErrorString(e));
+  return HARP_RA_OK;
+}
+
+// Transposed panel of the chunked K (or V): [B][H][DP][lp]
+int pack_chunks(const void* const* chunks, const int64_t* s, const Geometry& g, int batch, int h_num, int h_len,
+                bf16* dst, hipStream_t st) {
+  PackParams pp;
+  std::memset(&pp, 0, sizeof(pp));
+  int tiles = 0;
+  for (int c = 0; c < g.n; ++c) {
+    pp.src[c] = static_cast<const bf16*>(chunks[c]);
+    pp.len[c] = g.len[c];
+    pp.off[c] = g.off[c];
+    pp.tile0[c] = tiles;
+    tiles += (g.len[c] + 63) / 64;
+  }
+  pp.n = g.n;
+  pp.sb = s[0];
+  pp.sh = s[1];
+  pp.st = s[2];
+  pp.dst = dst;
+  pp.lp = g.lp;
+  pp.DP = padded_d(h_len);
+  pp.D = h_len;
+  pp.H = h_num;
+  pp.B = batch;
+  if (tiles == 0) return HARP_RA_OK;
+  TimedLaunch tl(HARP_RA_KERNEL_PACK, st);
+  return launched(launch_pack_t(pp, tiles, st), "pack");
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* harp_ra_last_error(void) { return g_last_error.c_str(); }
+
+const char* harp_ra_version(void) { return "harp_ra 0.1.0 (gfx950)"; }
+
+int harp_ra_timing_enable(int enable) {
+  timing().on = (enable != 0);
+  return ok();
+}
+
+int harp_ra_timing_read(double* ms, int* launches, int n_kinds) {
+  if (!ms || !launches || n_kinds < 1) return fail(HARP_RA_EINVAL, "timing_read needs output arrays");
+  for (int i = 0; i < n_kinds; ++i) {
+    ms[i] = 0.0;
+    launches[i] = 0;
+  }
+  Timing& t = timing();
+  int rc = HARP_RA_OK;
+  for (auto& r : t.recs) {
+    float e = 0.f;
+    if (hipEventElapsedTime(&e, r.a, r.b) != hipSuccess) rc = HARP_RA_ELAUNCH;
+    if (r.kind < n_kinds) {
+      ms[r.kind] += e;
+      launches[r.kind] += 1;
+    }
+    t.pool.push_back(r.a);
+    t.pool.push_back(r.b);
+  }
+  t.recs.clear();
+  if (rc) return fail(rc, "hipEventElapsedTime failed (were the streams synchronised?)");
+  return ok();
+}
+
+size_t harp_ra_forward_workspace_bytes(int batch, int h_num, int h_len, int sp_size, int kv_chunk_len,
+                                       const int32_t* kv_valid_lens) {
+  Geometry g;
+  if (check_dims(batch, h_num, 1, h_len) != HARP_RA_OK) return 0;
+  if (make_geometry(sp_size, kv_chunk_len, kv_valid_lens, &g) != HARP_RA_OK) return 0;
+  return fwd_ws(batch, h_num, h_len, g);
+}
+
+size_t harp_ra_backward_workspace_bytes(int batch, int h_num, int t_num, int h_len, int sp_size, int kv_chunk_len,
+                                        const int32_t* kv_valid_lens) {
+  Geometry g;
+  if (check_dims(batch, h_num, t_num, h_len) != HARP_RA_OK) return 0;
+  if (make_geometry(sp_size, kv_chunk_len, kv_valid_lens, &g) != HARP_RA_OK) return 0;
+  return bwd_ws(batch, h_num, t_num, h_len, g);
+}
+
+int harp_ra_forward(const void* q, const int64_t* q_strides, const void* const* k_chunks,
+                    const void* const* v_chunks, const int64_t* kv_strides, int kv_chunk_len,
+                    const int32_t* kv_valid_lens, float* out, const int64_t* out_strides, void* m_i, int m_i_dtype,
+                    float* l_i, int batch, int h_num, int t_num, int h_len, int sp_size, int ring_rank, float scale,
+                    void* workspace, size_t workspace_bytes, void* stream) {
+  int rc;
+  if ((rc = check_dims(batch, h_num, t_num, h_len))) return rc;
+  Geometry g;
+  if ((rc = make_geometry(sp_size, kv_chunk_len, kv_valid_lens, &g))) return rc;
+  if (ring_rank < 0 || ring_rank >= sp_size)
+    return fail(HARP_RA_EINVAL, "ring_rank=%d must be in [0, sp_size=%d)", ring_rank, sp_size);
+  if (!std::isfinite(scale)) return fail(HARP_RA_EINVAL, "scale must be finite");
+  if ((rc = check_bf16_view(q, q_strides, "q"))) return rc;
+  if (!k_chunks || !v_chunks) return fail(HARP_RA_EINVAL, "k_chunks / v_chunks are NULL");
+  for (int c = 0; c < sp_size; ++c) {
+    if ((rc = check_bf16_view(k_chunks[c], kv_strides, "k chunk"))) return rc;
+    if ((rc = check_bf16_view(v_chunks[c], kv_strides, "v chunk"))) return rc;
+  }
+  if ((rc = check_plain_view(out, out_strides, "out"))) return rc;
+  if (!m_i || !l_i) return fail(HARP_RA_EINVAL, "m_i / l_i are NULL");
+  if (m_i_dtype != HARP_RA_F32 && m_i_dtype != HARP_RA_BF16) return fail(HARP_RA_EINVAL, "m_i_dtype must be F32 or BF16");
+
+  const size_t need = fwd_ws(batch, h_num, h_len, g);
+  if ((rc = resolve_workspace(&workspace, &workspace_bytes, need))) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+
+  bf16* vt = static_cast<bf16*>(workspace);
+  if ((rc = pack_chunks(v_chunks, kv_strides, g, batch, h_num, h_len, vt, st))) return rc;
+
+  FwdParams p;
+  std::memset(&p, 0, sizeof(p));
+  p.q = static_cast<const bf16*>(q);
+  p.sqb = q_strides[0];
+  p.sqh = q_strides[1];
+  p.sqt = q_strides[2];
+  p.skb = kv_strides[0];
+  p.skh = kv_strides[1];
+  p.skt = kv_strides[2];
+  p.vt = vt;
+  p.out = out;
+  p.sob = out_strides[0];
+  p.soh = out_strides[1];
+  p.sot = out_strides[2];
+  p.m = m_i;
+  p.m_bf16 = (m_i_dtype == HARP_RA_BF16);
+  p.l = l_i;
+  p.B = batch;
+  p.H = h_num;
+  p.T = t_num;
+  p.D = h_len;
+  p.scale = scale;
+  p.ct.n = sp_size;
+  p.ct.lp = g.lp;
+  for (int c = 0; c < sp_size; ++c) {
+    p.ct.k[c] = static_cast<const bf16*>(k_chunks[c]);
+    p.ct.v[c] = static_cast<const bf16*>(v_chunks[c]);
+    p.ct.len[c] = g.len[c];
+    p.ct.off[c] = g.off[c];
+    p.ct.order[c] = (c + ring_rank) % sp_size;
+  }
+  {
+    TimedLaunch tl(HARP_RA_KERNEL_FWD, st);
+    if ((rc = launched(launch_fwd(p, st), "forward"))) return rc;
+  }
+  return ok();
+}
+
+int harp_ra_delta(const void* grad_out, const int64_t* do_strides, const float* out, const int64_t* out_strides,
+                  float* delta, int batch, int h_num, int t_num, int h_len, void* stream) {
+  int rc;
+  if ((rc = check_dims(batch, h_num, t_num, h_len))) return rc;
+  if ((rc = check_bf16_view(grad_out, do_strides, "grad_out"))) return rc;
+  if ((rc = check_plain_view(out, out_strides, "out"))) return rc;
+  if (!delta) return fail(HARP_RA_EINVAL, "delta is NULL");
+  DeltaParams p;
+  p.dout = static_cast<const bf16*>(grad_out);
+  p.sdb = do_strides[0];
+  p.sdh = do_strides[1];
+  p.sdt = do_strides[2];
+  p.out = out;
+  p.sob = out_strides[0];
+  p.soh = out_strides[1];
+  p.sot = out_strides[2];
+  p.delta = delta;
+  p.B = batch;
+  p.H = h_num;
+  p.T = t_num;
+  p.D = h_len;
+  {
+    TimedLaunch tl(HARP_RA_KERNEL_DELTA, static_cast<hipStream_t>(stream));
+    if ((rc = launched(launch_delta(p, static_cast<hipStream_t>(stream)), "delta"))) return rc;
+  }
+  return ok();
+}
+
+int harp_ra_backward(const void* q, const int64_t* q_strides, void* grad_q, const int64_t* dq_strides, int dq_dtype,
+                     const void* const* k_chunks, const void* const* v_chunks, const int64_t* kv_strides,
+                     void* const* dk_chunks, void* const* dv_chunks, const int64_t* dkv_strides, int dkv_dtype,
+                     int kv_chunk_len, const int32_t* kv_valid_lens, const void* grad_out, const int64_t* do_strides,
+                     const void* m_i, int m_i_dtype, const float* l_i, const float* delta, int batch, int h_num,
+                     int t_num, int h_len, int sp_size, int ring_rank, float scale, void* workspace,
+                     size_t workspace_bytes, void* stream) {
+  int rc;
+  if ((rc = check_dims(batch, h_num, t_num, h_len))) return rc;
+  Geometry g;
+  if ((rc = make_geometry(sp_size, kv_chunk_len, kv_valid_lens, &g))) return rc;
+  if (ring_rank < 0 || ring_rank >= sp_size)
+    return fail(HARP_RA_EINVAL, "ring_rank=%d must be in [0, sp_size=%d)", ring_rank, sp_size);
+  if (!std::isfinite(scale)) return fail(HARP_RA_EINVAL, "scale must be finite");
+  if ((rc = check_bf16_view(q, q_strides, "q"))) return rc;
+  if ((rc = check_bf16_view(grad_out, do_strides, "grad_out"))) return rc;
+  if ((rc = check_plain_view(grad_q, dq_strides, "grad_q"))) return rc;
+  if (dq_dtype != HARP_RA_F32 && dq_dtype != HARP_RA_BF16) return fail(HARP_RA_EINVAL, "dq_dtype must be F32 or BF16");
+  if (dkv_dtype != HARP_RA_F32 && dkv_dtype != HARP_RA_BF16)
+    return fail(HARP_RA_EINVAL, "dkv_dtype must be F32 or BF16");
+  if (!k_chunks || !v_chunks || !dk_chunks || !dv_chunks) return fail(HARP_RA_EINVAL, "chunk pointer arrays are NULL");
+  for (int c = 0; c < sp_size; ++c) {
+    if ((rc = check_bf16_view(k_chunks[c], kv_strides, "k chunk"))) return rc;
+    if ((rc = check_bf16_view(v_chunks[c], kv_strides, "v chunk"))) return rc;
+    if ((rc = check_plain_view(dk_chunks[c], dkv_strides, "dK chunk"))) return rc;
+    if ((rc = check_plain_view(dv_chunks[c], dkv_strides, "dV chunk"))) return rc;
+  }
+  if (!m_i || !l_i || !delta) return fail(HARP_RA_EINVAL, "m_i / l_i / delta are NULL");
+  if (m_i_dtype != HARP_RA_F32 && m_i_dtype != HARP_RA_BF16) return fail(HARP_RA_EINVAL, "m_i_dtype must be F32 or BF16");
+
+  const size_t need = bwd_ws(batch, h_num, t_num, h_len, g);
+  if ((rc = resolve_workspace(&workspace, &workspace_bytes, need))) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const size_t dp = padded_d(h_len);
+  char* ws = static_cast<char*>(workspace);
+  bf16* kt = reinterpret_cast<bf16*>(ws);
+  bf16* qt = reinterpret_cast<bf16*>(ws + align_up((size_t)batch * h_num * dp * g.lp * 2));
+  const size_t qt_bytes = align_up((size_t)batch * h_num * dp * round64(t_num) * 2);
+  bf16* gt = reinterpret_cast<bf16*>(reinterpret_cast<char*>(qt) + qt_bytes);
+
+  if ((rc = pack_chunks(k_chunks, kv_strides, g, batch, h_num, h_len, kt, st))) return rc;
+  Geometry gq;
+  gq.n = 1;
+  gq.len[0] = t_num;
+  gq.off[0] = 0;
+  gq.lp = round64(t_num);
+  if ((rc = pack_chunks(&q, q_strides, gq, batch, h_num, h_len, qt, st))) return rc;
+  if ((rc = pack_chunks(&grad_out, do_strides, gq, batch, h_num, h_len, gt, st))) return rc;
+
+  BwdParams p;
+  std::memset(&p, 0, sizeof(p));
+  p.q = static_cast<const bf16*>(q);
+  p.sqb = q_strides[0];
+  p.sqh = q_strides[1];
+  p.sqt = q_strides[2];
+  p.dout = static_cast<const bf16*>(grad_out);
+  p.sdb = do_strides[0];
+  p.sdh = do_strides[1];
+  p.sdt = do_strides[2];
+  p.skb = kv_strides[0];
+  p.skh = kv_strides[1];
+  p.skt = kv_strides[2];
+  p.sdkb = dkv_strides[0];
+  p.sdkh = dkv_strides[1];
+  p.sdkt = dkv_strides[2];
+  p.dkv_f32 = (dkv_dtype == HARP_RA_F32);
+  p.dq = grad_q;
+  p.sdqb = dq_strides[0];
+  p.sdqh = dq_strides[1];
+  p.sdqt = dq_strides[2];
+  p.dq_f32 = (dq_dtype == HARP_RA_F32);
+  p.m = m_i;
+  p.m_bf16 = (m_i_dtype == HARP_RA_BF16);
+  p.l = l_i;
+  p.delta = delta;
+  p.kt = kt;
+  p.qt = qt;
+  p.gt = gt;
+  p.tp = round64(t_num);
+  p.B = batch;
+  p.H = h_num;
+  p.T = t_num;
+  p.D = h_len;
+  p.scale = scale;
+  p.ct.n = sp_size;
+  p.ct.lp = g.lp;
+  int key_tiles = 0;
+  for (int c = 0; c < sp_size; ++c) {
+    p.ct.k[c] = static_cast<const bf16*>(k_chunks[c]);
+    p.ct.v[c] = static_cast<const bf16*>(v_chunks[c]);
+    p.ct.dk[c] = static_cast<bf16*>(dk_chunks[c]);
+    p.ct.dv[c] = static_cast<bf16*>(dv_chunks[c]);
+    p.ct.len[c] = g.len[c];
+    p.ct.off[c] = g.off[c];
+    p.ct.order[c] = (c + ring_rank) % sp_size;
+    p.ct.tile0[c] = key_tiles;
+    p.ct_rows[c] = kv_chunk_len;
+    key_tiles += (kv_chunk_len + 127) / 128;
+  }
+  {
+    TimedLaunch tl(HARP_RA_KERNEL_DKDV, st);
+    if ((rc = launched(launch_dkdv(p, key_tiles, st), "dK/dV"))) return rc;
+  }
+  {
+    TimedLaunch tl(HARP_RA_KERNEL_DQ, st);
+    if ((rc = launched(launch_dq(p, st), "dQ"))) return rc;
+  }
+  return ok();
+}
+
+}  // extern "C"

@@ -1,0 +1,65 @@
+// Shared device-side definitions for the gfx950 ring-attention kernels.
+//
+// Layout conventions (CDNA4 wave64 MFMA, v_mfma_f32_32x32x16_bf16):
+//   A operand: lane l holds A[row = l%32][k-set of 8 picked by l/32]
+//   B operand: lane l holds B[k-set of 8 picked by l/32][col = l%32]
+//   C/D (16 fp32 per lane): C[row = 8*(r/4) + 4*(l/32) + r%4][col = l%32]
+// A and B of one instruction always use the same k-set for a lane, so the
+// order of k inside a k-step is free; the kernels exploit that to feed a
+// C-layout accumulator (16 rows per lane) straight back as the next GEMM's
+// k-operand without any lane shuffle.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace harp_ra {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kMaxChunks = 16;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// Per-call description of the N KV chunks of the ring (passed by value).
+struct ChunkTable {
+  const bf16* k[kMaxChunks];  // chunk base pointers ([B,H,Tc,D] views, shared strides)
+  const bf16* v[kMaxChunks];
+  bf16* dk[kMaxChunks];       // backward outputs (same strides as dkv_strides)
+  bf16* dv[kMaxChunks];
+  int len[kMaxChunks];        // valid keys of chunk c
+  int off[kMaxChunks];        // column offset of chunk c inside packed [D][Lp] buffers
+  int tile0[kMaxChunks];      // first flat key-tile index of chunk c (backward grid)
+  int order[kMaxChunks];      // ring order: chunk visited at step s
+  int n;                      // number of chunks (sp_size)
+  int lp;                     // total padded key columns of the packed buffers
+};
+
+__device__ __forceinline__ f32x16 mfma32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.f;
+  return z;
+}
+
+__device__ __forceinline__ bf16x8 zero8() {
+  bf16x8 z;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) z[i] = (bf16)0.f;
+  return z;
+}
+
+// Row of the 32x32 C layout held in accumulator register r by lane-half g.
+__device__ __forceinline__ constexpr int c_row(int r, int g) { return 8 * (r >> 2) + 4 * g + (r & 3); }
+
+}  // namespace harp_ra

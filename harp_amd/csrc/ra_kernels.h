@@ -1,0 +1,78 @@
+// Kernel parameter blocks and host launchers (internal to libharp_ra.so).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "ra_common.h"
+
+namespace harp_ra {
+
+struct PackParams {
+  const bf16* src[kMaxChunks];  // per-chunk [B,H,rows,D] views
+  int len[kMaxChunks];          // valid rows of chunk c
+  int off[kMaxChunks];          // destination column of chunk c
+  int tile0[kMaxChunks];        // first flat 64-row tile of chunk c
+  int n;
+  int64_t sb, sh, st;           // source strides (elements), d stride 1
+  bf16* dst;                    // [B][H][DP][lp]
+  int lp, DP, D, H, B;
+};
+
+struct FwdParams {
+  const bf16* q;
+  int64_t sqb, sqh, sqt;
+  int64_t skb, skh, skt;  // strides shared by every K/V chunk
+  const bf16* vt;         // packed V^T panels [B][H][DP][ct.lp]
+  float* out;
+  int64_t sob, soh, sot;
+  void* m;                // [B,H,T] contiguous, fp32 or bf16
+  int m_bf16;
+  float* l;               // [B,H,T] contiguous
+  int B, H, T, D;
+  float scale;
+  ChunkTable ct;
+};
+
+struct DeltaParams {
+  const bf16* dout;
+  int64_t sdb, sdh, sdt;
+  const float* out;
+  int64_t sob, soh, sot;
+  float* delta;  // [B,H,T] contiguous
+  int B, H, T, D;
+};
+
+struct BwdParams {
+  const bf16* q;
+  int64_t sqb, sqh, sqt;
+  const bf16* dout;
+  int64_t sdb, sdh, sdt;
+  int64_t skb, skh, skt;       // K/V chunk strides
+  int64_t sdkb, sdkh, sdkt;    // dK/dV chunk strides
+  int dkv_f32;
+  void* dq;
+  int64_t sdqb, sdqh, sdqt;
+  int dq_f32;
+  const void* m;
+  int m_bf16;
+  const float* l;
+  const float* delta;
+  const bf16* kt;  // packed K^T panels [B][H][DP][ct.lp]
+  const bf16* qt;  // packed Q^T panels [B][H][DP][tp]
+  const bf16* gt;  // packed dO^T panels [B][H][DP][tp]
+  int tp;
+  int ct_rows[kMaxChunks];  // stored rows of chunk c (dK/dV rows written, pads get 0)
+  int B, H, T, D;
+  float scale;
+  ChunkTable ct;
+};
+
+int padded_d(int D);
+hipError_t launch_pack_t(const PackParams& p, int n_tiles, hipStream_t st);
+hipError_t launch_fwd(const FwdParams& p, hipStream_t st);
+hipError_t launch_delta(const DeltaParams& p, hipStream_t st);
+hipError_t launch_dq(const BwdParams& p, hipStream_t st);
+hipError_t launch_dkdv(const BwdParams& p, int n_key_tiles, hipStream_t st);
+
+}  // namespace harp_ra

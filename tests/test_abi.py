@@ -1,0 +1,138 @@
+"""CPU tests of the boundary: the C-ABI library loads and exports every
+function include/harp_ring_attn.h declares, validates arguments on the host
+before touching a device, sizes its workspace, and the operator library
+registers the reference's schemas (no GPU needed)."""
+
+import ctypes
+import math
+import os
+import re
+import subprocess
+
+import pytest
+import torch
+
+import harp_amd
+from harp_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "harp_ring_attn.h")
+
+REF_FWD_SCHEMA = ("ring_attention_forward(Tensor q, Tensor k, Tensor v, Tensor(a!) out, Tensor(b!) m_i, "
+                  "Tensor(c!) l_i, int sp_size, float scale")
+REF_BWD_SCHEMA = ("ring_attention_backward(Tensor q, Tensor(a!) grad_q, Tensor k, Tensor(b!) dK, Tensor v, "
+                  "Tensor(c!) dV, Tensor grad_out, Tensor m_i, Tensor l_i, Tensor D, int sp_size, float scale")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"HARP_RA_API\s+[\w\s\*]+?\b(harp_ra_\w+)\s*\(", text)))
+
+
+def test_header_declares_expected_entry_points():
+    fns = header_functions()
+    for name in ("harp_ra_forward", "harp_ra_backward", "harp_ra_delta"):
+        assert name in fns
+    assert set(fns) == set(_lib.ABI_PROTOTYPES), "ctypes prototypes must cover exactly the header"
+
+
+def test_library_exports_every_declared_symbol():
+    lib = harp_amd.load_abi()
+    for name in header_functions():
+        assert hasattr(lib, name), name
+    nm = subprocess.run(["nm", "-D", "--defined-only", str(_lib.ABI_LIB)], capture_output=True, text=True)
+    exported = {ln.split()[-1] for ln in nm.stdout.splitlines() if " T " in ln}
+    ours = {s for s in exported if s.startswith("harp_ra_")}
+    assert ours == set(header_functions()), ours ^ set(header_functions())
+    assert lib.harp_ra_version().decode().startswith("harp_ra")
+
+
+def _fwd_call(**over):
+    lib = harp_amd.load_abi()
+    st = _lib.i64_array([8 * 64 * 128, 64, 8 * 64, 1])
+    fake = 1 << 20  # never dereferenced: validation fails first
+    a = dict(q=fake, qs=st, kc=_lib.ptr_array([fake]), vc=_lib.ptr_array([fake]), ks=st, tc=128, lens=None,
+             out=fake, os=st, m=fake, mdt=_lib.HARP_RA_BF16, l=fake, B=1, H=8, T=128, D=64, sp=1, rank=0,
+             scale=0.125, ws=fake, wsb=1 << 30, stream=None)
+    a.update(over)
+    return lib.harp_ra_forward(a["q"], a["qs"], a["kc"], a["vc"], a["ks"], a["tc"], a["lens"], a["out"], a["os"],
+                               a["m"], a["mdt"], a["l"], a["B"], a["H"], a["T"], a["D"], a["sp"], a["rank"],
+                               a["scale"], a["ws"], a["wsb"], a["stream"])
+
+
+@pytest.mark.parametrize(
+    "over,code,msg",
+    [
+        (dict(T=0), _lib.HARP_RA_EINVAL, "sizes must be positive"),
+        (dict(D=60), _lib.HARP_RA_EUNSUPPORTED, "multiple of 8"),
+        (dict(D=136), _lib.HARP_RA_EUNSUPPORTED, "> 128"),
+        (dict(sp=0), _lib.HARP_RA_EINVAL, "sp_size"),
+        (dict(sp=17), _lib.HARP_RA_EINVAL, "sp_size"),
+        (dict(rank=1), _lib.HARP_RA_EINVAL, "ring_rank"),
+        (dict(q=None), _lib.HARP_RA_EINVAL, "q is NULL"),
+        (dict(q=(1 << 20) + 2), _lib.HARP_RA_EINVAL, "16-byte aligned"),
+        (dict(qs=_lib.i64_array([8 * 64 * 128, 64, 8 * 64, 2])), _lib.HARP_RA_EINVAL, "unit stride"),
+        (dict(qs=_lib.i64_array([8 * 64 * 128, 60, 8 * 64, 1])), _lib.HARP_RA_EINVAL, "multiple of 8"),
+        (dict(lens=_lib.i32_array([129])), _lib.HARP_RA_EINVAL, "kv_valid_lens"),
+        (dict(mdt=7), _lib.HARP_RA_EINVAL, "m_i_dtype"),
+        (dict(scale=float("nan")), _lib.HARP_RA_EINVAL, "scale"),
+        (dict(wsb=16), _lib.HARP_RA_ENOMEM, "workspace"),
+    ],
+)
+def test_forward_rejects_bad_arguments_before_any_device_call(over, code, msg):
+    rc = _fwd_call(**over)
+    assert rc == code
+    assert msg in _lib.last_error()
+
+
+def test_workspace_sizes():
+    fwd = harp_amd.forward_workspace_bytes(1, 24, 128, 8, 8192)
+    assert fwd == 1 * 24 * 128 * 8 * 8192 * 2
+    bwd = harp_amd.backward_workspace_bytes(1, 24, 8192, 128, 8, 8192)
+    assert bwd == 24 * 128 * 65536 * 2 + 2 * 24 * 128 * 8192 * 2
+    # D=72 pads panels to 96 rows; ragged chunk lengths round up to 64 keys
+    assert harp_amd.forward_workspace_bytes(2, 16, 72, 4, 4480, [4429] * 4) == 2 * 16 * 96 * 4 * 4480 * 2
+    assert harp_amd.forward_workspace_bytes(1, 1, 64, 0, 64) == 0
+    assert harp_amd.forward_workspace_bytes(1, 1, 66, 1, 64) == 0
+
+
+def test_timing_read_validates_arguments():
+    lib = harp_amd.load_abi()
+    assert lib.harp_ra_timing_read(None, None, 5) == _lib.HARP_RA_EINVAL
+    assert lib.harp_ra_timing_enable(0) == _lib.HARP_RA_OK
+    t = _lib.timing_read()
+    assert set(t) == set(_lib.KERNEL_KINDS) and all(v == (0.0, 0) for v in t.values())
+
+
+def test_operator_library_registers_reference_schemas():
+    harp_amd.load_ops()
+    f = str(torch.ops.ring_attention_ops.ring_attention_forward.default._schema)
+    b = str(torch.ops.ring_attention_ops.ring_attention_backward.default._schema)
+    assert f.startswith("ring_attention_ops::" + REF_FWD_SCHEMA)
+    assert b.startswith("ring_attention_ops::" + REF_BWD_SCHEMA)
+    # reference positional calls stay valid: only defaulted trailing args were added
+    assert f.endswith("int ring_rank=0, int[]? kv_lens=None) -> (Tensor(a!), Tensor(b!), Tensor(c!))")
+    assert b.endswith("int ring_rank=0, int[]? kv_lens=None) -> (Tensor(a!), Tensor(b!), Tensor(c!))")
+
+
+def test_cpu_tensors_raise_instead_of_falling_back():
+    harp_amd.load_ops()
+    q = torch.zeros(1, 2, 16, 64, dtype=torch.bfloat16)
+    out = torch.zeros(1, 2, 16, 64)
+    m = torch.zeros(1, 2, 16, 1, dtype=torch.bfloat16)
+    l = torch.zeros(1, 2, 16, 1)
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        torch.ops.ring_attention_ops.ring_attention_forward(q, q, q, out, m, l, 1, 0.125)
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        torch.ops.ring_attention_ops.ring_attention_delta(q, out)
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        torch.ops.ring_attention_ops.ring_attention_backward(q, q, q, q, q, q, q, l, l, l, 1, 0.125)
+
+
+def test_product_package_never_imports_the_oracle():
+    pkg = os.path.join(ROOT, "harp_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for fn in files:
+            if fn.endswith((".py", ".cpp", ".hip", ".h")):
+                text = open(os.path.join(dirpath, fn)).read()
+                assert "oracle" not in text.replace("oracle/", "").lower() or fn == "build.py", fn
