@@ -1,14 +1,16 @@
-// C ABI of libharp_ra.so: argument validation, workspace carving and kernel
-// sequencing for the ring-attention block.  See include/harp_ring_attn.h.
+// C ABI of libharp_ra.so: argument validation, kernel sequencing and optional
+// kernel timing for the ring-attention block.  See include/harp_ring_attn.h.
 //
 // Host flow mirrors the reference's operator bodies:
-//   forward  (ring_attn.cpp:2412-2575): pack V panels (:2452-2485) -> ring loop
-//            over all chunks (:2488-2568) -> O /= l (:2569-2573), here one
-//            pack launch + one fused kernel launch.
-//   backward (ring_attn.cpp:2577-2829): pack Q/dO/K panels (:2664-2717) ->
-//            per-chunk S/dP recompute, dQ/dK/dV (:2723-2816) -> dQ owner sum
-//            (:2817-2828), here pack launches + a dK/dV kernel and a dQ kernel
-//            whose fp32 register accumulators replace the dQ slot reduction.
+//   forward  (ring_attn.cpp:2412-2575): the reference packs K/V/Q into SME
+//            panels (:2452-2485) and then loops over ring steps (:2488-2568)
+//            and normalises (:2569-2573); here a single fused kernel launch
+//            streams every chunk's K/V tiles through LDS (no panel copies).
+//   backward (ring_attn.cpp:2577-2829): packs (:2664-2717), per-step S/dP
+//            recompute and dQ/dK/dV GEMMs (:2723-2816), dQ owner sum
+//            (:2817-2828); here a dK/dV kernel (KV-stationary, like the
+//            reference) and a dQ kernel whose fp32 register accumulators
+//            replace the dQ slot reduction.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -44,9 +46,6 @@ int ok() {
   return HARP_RA_OK;
 }
 
-constexpr size_t kAlign = 256;
-size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
-int round64(int x) { return (x + 63) / 64 * 64; }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
@@ -86,39 +85,26 @@ int check_dims(int batch, int h_num, int t_num, int h_len) {
 struct Geometry {
   int n = 0;
   int len[kMaxChunks] = {};
-  int off[kMaxChunks] = {};
-  int lp = 0;
 };
 
 int make_geometry(int sp_size, int kv_chunk_len, const int32_t* kv_valid_lens, Geometry* g) {
   if (sp_size < 1 || sp_size > HARP_RA_MAX_CHUNKS)
     return fail(HARP_RA_EINVAL, "sp_size=%d must be in [1, %d]", sp_size, HARP_RA_MAX_CHUNKS);
   if (kv_chunk_len < 1) return fail(HARP_RA_EINVAL, "kv_chunk_len=%d must be positive", kv_chunk_len);
+  if (kv_chunk_len > (1 << 26)) return fail(HARP_RA_EUNSUPPORTED, "kv_chunk_len=%d is too large", kv_chunk_len);
   g->n = sp_size;
-  int64_t lp = 0;
   for (int c = 0; c < sp_size; ++c) {
     const int len = kv_valid_lens ? kv_valid_lens[c] : kv_chunk_len;
     if (len < 0 || len > kv_chunk_len)
       return fail(HARP_RA_EINVAL, "kv_valid_lens[%d]=%d must be in [0, kv_chunk_len=%d]", c, len, kv_chunk_len);
     g->len[c] = len;
-    g->off[c] = (int)lp;
-    lp += round64(len);
   }
-  if (lp == 0) lp = 64;  // keep panels non-empty
-  if (lp > (int64_t)1 << 30) return fail(HARP_RA_EUNSUPPORTED, "total KV length too large");
-  g->lp = (int)lp;
   return HARP_RA_OK;
 }
 
-size_t fwd_ws(int batch, int h_num, int h_len, const Geometry& g) {
-  return align_up((size_t)batch * h_num * padded_d(h_len) * g.lp * 2);
-}
-size_t bwd_ws(int batch, int h_num, int t_num, int h_len, const Geometry& g) {
-  const size_t dp = padded_d(h_len);
-  const size_t kt = align_up((size_t)batch * h_num * dp * g.lp * 2);
-  const size_t qt = align_up((size_t)batch * h_num * dp * round64(t_num) * 2);
-  return kt + 2 * qt;
-}
+// The kernels stage every operand through LDS and need no device scratch.
+size_t fwd_ws(int, int, int, const Geometry&) { return 0; }
+size_t bwd_ws(int, int, int, int, const Geometry&) { return 0; }
 
 // Library-owned grow-only workspace, one per device (used when the caller
 // passes workspace == NULL).
@@ -133,6 +119,7 @@ OwnedWorkspace& owned() {
 }
 
 int resolve_workspace(void** ws, size_t* ws_bytes, size_t need) {
+  if (need == 0) return HARP_RA_OK;
   if (*ws) {
     if (*ws_bytes < need)
       return fail(HARP_RA_ENOMEM, "workspace of %zu bytes is smaller than the %zu bytes needed", *ws_bytes, need);
@@ -212,34 +199,6 @@ int launched(hipError_t e, const char* what) {
   return HARP_RA_OK;
 }
 
-// Transposed panel of the chunked K (or V): [B][H][DP][lp]
-int pack_chunks(const void* const* chunks, const int64_t* s, const Geometry& g, int batch, int h_num, int h_len,
-                bf16* dst, hipStream_t st) {
-  PackParams pp;
-  std::memset(&pp, 0, sizeof(pp));
-  int tiles = 0;
-  for (int c = 0; c < g.n; ++c) {
-    pp.src[c] = static_cast<const bf16*>(chunks[c]);
-    pp.len[c] = g.len[c];
-    pp.off[c] = g.off[c];
-    pp.tile0[c] = tiles;
-    tiles += (g.len[c] + 63) / 64;
-  }
-  pp.n = g.n;
-  pp.sb = s[0];
-  pp.sh = s[1];
-  pp.st = s[2];
-  pp.dst = dst;
-  pp.lp = g.lp;
-  pp.DP = padded_d(h_len);
-  pp.D = h_len;
-  pp.H = h_num;
-  pp.B = batch;
-  if (tiles == 0) return HARP_RA_OK;
-  TimedLaunch tl(HARP_RA_KERNEL_PACK, st);
-  return launched(launch_pack_t(pp, tiles, st), "pack");
-}
-
 }  // namespace
 
 extern "C" {
@@ -279,16 +238,16 @@ int harp_ra_timing_read(double* ms, int* launches, int n_kinds) {
 size_t harp_ra_forward_workspace_bytes(int batch, int h_num, int h_len, int sp_size, int kv_chunk_len,
                                        const int32_t* kv_valid_lens) {
   Geometry g;
-  if (check_dims(batch, h_num, 1, h_len) != HARP_RA_OK) return 0;
-  if (make_geometry(sp_size, kv_chunk_len, kv_valid_lens, &g) != HARP_RA_OK) return 0;
+  if (check_dims(batch, h_num, 1, h_len) != HARP_RA_OK) return SIZE_MAX;
+  if (make_geometry(sp_size, kv_chunk_len, kv_valid_lens, &g) != HARP_RA_OK) return SIZE_MAX;
   return fwd_ws(batch, h_num, h_len, g);
 }
 
 size_t harp_ra_backward_workspace_bytes(int batch, int h_num, int t_num, int h_len, int sp_size, int kv_chunk_len,
                                         const int32_t* kv_valid_lens) {
   Geometry g;
-  if (check_dims(batch, h_num, t_num, h_len) != HARP_RA_OK) return 0;
-  if (make_geometry(sp_size, kv_chunk_len, kv_valid_lens, &g) != HARP_RA_OK) return 0;
+  if (check_dims(batch, h_num, t_num, h_len) != HARP_RA_OK) return SIZE_MAX;
+  if (make_geometry(sp_size, kv_chunk_len, kv_valid_lens, &g) != HARP_RA_OK) return SIZE_MAX;
   return bwd_ws(batch, h_num, t_num, h_len, g);
 }
 
@@ -303,7 +262,7 @@ int harp_ra_forward(const void* q, const int64_t* q_strides, const void* const* 
   if ((rc = make_geometry(sp_size, kv_chunk_len, kv_valid_lens, &g))) return rc;
   if (ring_rank < 0 || ring_rank >= sp_size)
     return fail(HARP_RA_EINVAL, "ring_rank=%d must be in [0, sp_size=%d)", ring_rank, sp_size);
-  if (!std::isfinite(scale)) return fail(HARP_RA_EINVAL, "scale must be finite");
+  if (!std::isfinite(scale) || !(scale > 0.f)) return fail(HARP_RA_EINVAL, "scale must be finite and positive");
   if ((rc = check_bf16_view(q, q_strides, "q"))) return rc;
   if (!k_chunks || !v_chunks) return fail(HARP_RA_EINVAL, "k_chunks / v_chunks are NULL");
   for (int c = 0; c < sp_size; ++c) {
@@ -318,9 +277,6 @@ int harp_ra_forward(const void* q, const int64_t* q_strides, const void* const* 
   if ((rc = resolve_workspace(&workspace, &workspace_bytes, need))) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
 
-  bf16* vt = static_cast<bf16*>(workspace);
-  if ((rc = pack_chunks(v_chunks, kv_strides, g, batch, h_num, h_len, vt, st))) return rc;
-
   FwdParams p;
   std::memset(&p, 0, sizeof(p));
   p.q = static_cast<const bf16*>(q);
@@ -330,7 +286,6 @@ int harp_ra_forward(const void* q, const int64_t* q_strides, const void* const* 
   p.skb = kv_strides[0];
   p.skh = kv_strides[1];
   p.skt = kv_strides[2];
-  p.vt = vt;
   p.out = out;
   p.sob = out_strides[0];
   p.soh = out_strides[1];
@@ -344,12 +299,10 @@ int harp_ra_forward(const void* q, const int64_t* q_strides, const void* const* 
   p.D = h_len;
   p.scale = scale;
   p.ct.n = sp_size;
-  p.ct.lp = g.lp;
   for (int c = 0; c < sp_size; ++c) {
     p.ct.k[c] = static_cast<const bf16*>(k_chunks[c]);
     p.ct.v[c] = static_cast<const bf16*>(v_chunks[c]);
     p.ct.len[c] = g.len[c];
-    p.ct.off[c] = g.off[c];
     p.ct.order[c] = (c + ring_rank) % sp_size;
   }
   {
@@ -400,7 +353,7 @@ int harp_ra_backward(const void* q, const int64_t* q_strides, void* grad_q, cons
   if ((rc = make_geometry(sp_size, kv_chunk_len, kv_valid_lens, &g))) return rc;
   if (ring_rank < 0 || ring_rank >= sp_size)
     return fail(HARP_RA_EINVAL, "ring_rank=%d must be in [0, sp_size=%d)", ring_rank, sp_size);
-  if (!std::isfinite(scale)) return fail(HARP_RA_EINVAL, "scale must be finite");
+  if (!std::isfinite(scale) || !(scale > 0.f)) return fail(HARP_RA_EINVAL, "scale must be finite and positive");
   if ((rc = check_bf16_view(q, q_strides, "q"))) return rc;
   if ((rc = check_bf16_view(grad_out, do_strides, "grad_out"))) return rc;
   if ((rc = check_plain_view(grad_q, dq_strides, "grad_q"))) return rc;
@@ -420,21 +373,6 @@ int harp_ra_backward(const void* q, const int64_t* q_strides, void* grad_q, cons
   const size_t need = bwd_ws(batch, h_num, t_num, h_len, g);
   if ((rc = resolve_workspace(&workspace, &workspace_bytes, need))) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const size_t dp = padded_d(h_len);
-  char* ws = static_cast<char*>(workspace);
-  bf16* kt = reinterpret_cast<bf16*>(ws);
-  bf16* qt = reinterpret_cast<bf16*>(ws + align_up((size_t)batch * h_num * dp * g.lp * 2));
-  const size_t qt_bytes = align_up((size_t)batch * h_num * dp * round64(t_num) * 2);
-  bf16* gt = reinterpret_cast<bf16*>(reinterpret_cast<char*>(qt) + qt_bytes);
-
-  if ((rc = pack_chunks(k_chunks, kv_strides, g, batch, h_num, h_len, kt, st))) return rc;
-  Geometry gq;
-  gq.n = 1;
-  gq.len[0] = t_num;
-  gq.off[0] = 0;
-  gq.lp = round64(t_num);
-  if ((rc = pack_chunks(&q, q_strides, gq, batch, h_num, h_len, qt, st))) return rc;
-  if ((rc = pack_chunks(&grad_out, do_strides, gq, batch, h_num, h_len, gt, st))) return rc;
 
   BwdParams p;
   std::memset(&p, 0, sizeof(p));
@@ -462,17 +400,12 @@ int harp_ra_backward(const void* q, const int64_t* q_strides, void* grad_q, cons
   p.m_bf16 = (m_i_dtype == HARP_RA_BF16);
   p.l = l_i;
   p.delta = delta;
-  p.kt = kt;
-  p.qt = qt;
-  p.gt = gt;
-  p.tp = round64(t_num);
   p.B = batch;
   p.H = h_num;
   p.T = t_num;
   p.D = h_len;
   p.scale = scale;
   p.ct.n = sp_size;
-  p.ct.lp = g.lp;
   int key_tiles = 0;
   for (int c = 0; c < sp_size; ++c) {
     p.ct.k[c] = static_cast<const bf16*>(k_chunks[c]);
@@ -480,15 +413,17 @@ int harp_ra_backward(const void* q, const int64_t* q_strides, void* grad_q, cons
     p.ct.dk[c] = static_cast<bf16*>(dk_chunks[c]);
     p.ct.dv[c] = static_cast<bf16*>(dv_chunks[c]);
     p.ct.len[c] = g.len[c];
-    p.ct.off[c] = g.off[c];
     p.ct.order[c] = (c + ring_rank) % sp_size;
     p.ct.tile0[c] = key_tiles;
     p.ct_rows[c] = kv_chunk_len;
     key_tiles += (kv_chunk_len + 127) / 128;
   }
+  p.n_key_tiles = key_tiles;
+  if ((int64_t)key_tiles * h_num * batch > INT32_MAX || (int64_t)((t_num + 127) / 128) * h_num * batch > INT32_MAX)
+    return fail(HARP_RA_EUNSUPPORTED, "grid too large");
   {
     TimedLaunch tl(HARP_RA_KERNEL_DKDV, st);
-    if ((rc = launched(launch_dkdv(p, key_tiles, st), "dK/dV"))) return rc;
+    if ((rc = launched(launch_dkdv(p, st), "dK/dV"))) return rc;
   }
   {
     TimedLaunch tl(HARP_RA_KERNEL_DQ, st);

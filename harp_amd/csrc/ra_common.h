@@ -32,11 +32,9 @@ struct ChunkTable {
   bf16* dk[kMaxChunks];       // backward outputs (same strides as dkv_strides)
   bf16* dv[kMaxChunks];
   int len[kMaxChunks];        // valid keys of chunk c
-  int off[kMaxChunks];        // column offset of chunk c inside packed [D][Lp] buffers
-  int tile0[kMaxChunks];      // first flat key-tile index of chunk c (backward grid)
+  int tile0[kMaxChunks];      // first 128-key tile index of chunk c (backward grid)
   int order[kMaxChunks];      // ring order: chunk visited at step s
   int n;                      // number of chunks (sp_size)
-  int lp;                     // total padded key columns of the packed buffers
 };
 
 __device__ __forceinline__ f32x16 mfma32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {

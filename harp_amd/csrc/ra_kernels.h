@@ -8,22 +8,10 @@
 
 namespace harp_ra {
 
-struct PackParams {
-  const bf16* src[kMaxChunks];  // per-chunk [B,H,rows,D] views
-  int len[kMaxChunks];          // valid rows of chunk c
-  int off[kMaxChunks];          // destination column of chunk c
-  int tile0[kMaxChunks];        // first flat 64-row tile of chunk c
-  int n;
-  int64_t sb, sh, st;           // source strides (elements), d stride 1
-  bf16* dst;                    // [B][H][DP][lp]
-  int lp, DP, D, H, B;
-};
-
 struct FwdParams {
   const bf16* q;
   int64_t sqb, sqh, sqt;
   int64_t skb, skh, skt;  // strides shared by every K/V chunk
-  const bf16* vt;         // packed V^T panels [B][H][DP][ct.lp]
   float* out;
   int64_t sob, soh, sot;
   void* m;                // [B,H,T] contiguous, fp32 or bf16
@@ -58,21 +46,16 @@ struct BwdParams {
   int m_bf16;
   const float* l;
   const float* delta;
-  const bf16* kt;  // packed K^T panels [B][H][DP][ct.lp]
-  const bf16* qt;  // packed Q^T panels [B][H][DP][tp]
-  const bf16* gt;  // packed dO^T panels [B][H][DP][tp]
-  int tp;
+  int n_key_tiles;          // 128-key tiles per (b, h) over all chunks
   int ct_rows[kMaxChunks];  // stored rows of chunk c (dK/dV rows written, pads get 0)
   int B, H, T, D;
   float scale;
   ChunkTable ct;
 };
 
-int padded_d(int D);
-hipError_t launch_pack_t(const PackParams& p, int n_tiles, hipStream_t st);
 hipError_t launch_fwd(const FwdParams& p, hipStream_t st);
 hipError_t launch_delta(const DeltaParams& p, hipStream_t st);
 hipError_t launch_dq(const BwdParams& p, hipStream_t st);
-hipError_t launch_dkdv(const BwdParams& p, int n_key_tiles, hipStream_t st);
+hipError_t launch_dkdv(const BwdParams& p, hipStream_t st);
 
 }  // namespace harp_ra

@@ -96,9 +96,11 @@ Chunks split_chunks(const at::Tensor& q, const at::Tensor& k, const at::Tensor& 
   return c;
 }
 
+// Device scratch from the caching allocator (empty when none is needed).
 at::Tensor workspace(size_t bytes, const at::Tensor& like) {
-  return at::empty({static_cast<int64_t>(bytes > 0 ? bytes : 1)}, like.options().dtype(at::kByte));
+  return at::empty({static_cast<int64_t>(bytes)}, like.options().dtype(at::kByte));
 }
+void* ws_ptr(const at::Tensor& ws) { return ws.numel() ? ws.data_ptr() : nullptr; }
 
 std::tuple<at::Tensor, at::Tensor, at::Tensor> forward_hip(const at::Tensor& q, const at::Tensor& k,
                                                            const at::Tensor& v, at::Tensor out, at::Tensor m_i,
@@ -124,14 +126,14 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> forward_hip(const at::Tensor& q, 
   const int B = q.size(0), H = q.size(1), T = q.size(2), D = q.size(3);
   const int32_t* lens = ch.lens.empty() ? nullptr : ch.lens.data();
   const size_t ws_bytes = harp_ra_forward_workspace_bytes(B, H, D, sp_size, ch.chunk_len, lens);
-  check_status(ws_bytes ? HARP_RA_OK : HARP_RA_EINVAL, "ring_attention_forward");
+  check_status(ws_bytes != SIZE_MAX ? HARP_RA_OK : HARP_RA_EINVAL, "ring_attention_forward");
   at::Tensor ws = workspace(ws_bytes, q);
   const auto qs = strides4(q), ks = strides4(k), os = strides4(out);
   hipStream_t stream = c10::hip::getCurrentHIPStream(q.get_device()).stream();
   const int rc = harp_ra_forward(q.data_ptr(), qs.data(), ch.k.data(), ch.v.data(), ks.data(), ch.chunk_len, lens,
                                  out.data_ptr<float>(), os.data(), m_i.data_ptr(), m_code, l_i.data_ptr<float>(), B,
                                  H, T, D, static_cast<int>(sp_size), static_cast<int>(ring_rank),
-                                 static_cast<float>(scale), ws.data_ptr(), ws_bytes, stream);
+                                 static_cast<float>(scale), ws_ptr(ws), ws_bytes, stream);
   check_status(rc, "ring_attention_forward");
   return std::make_tuple(out, m_i, l_i);
 }
@@ -171,7 +173,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> backward_hip(const at::Tensor& q,
   const int B = q.size(0), H = q.size(1), T = q.size(2), Dh = q.size(3);
   const int32_t* lens = ch.lens.empty() ? nullptr : ch.lens.data();
   const size_t ws_bytes = harp_ra_backward_workspace_bytes(B, H, T, Dh, sp_size, ch.chunk_len, lens);
-  check_status(ws_bytes ? HARP_RA_OK : HARP_RA_EINVAL, "ring_attention_backward");
+  check_status(ws_bytes != SIZE_MAX ? HARP_RA_OK : HARP_RA_EINVAL, "ring_attention_backward");
   at::Tensor ws = workspace(ws_bytes, q);
   const auto qs = strides4(q), dqs = strides4(grad_q), ks = strides4(k), dks = strides4(dK), gs = strides4(grad_out);
   hipStream_t stream = c10::hip::getCurrentHIPStream(q.get_device()).stream();
@@ -179,7 +181,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> backward_hip(const at::Tensor& q,
       q.data_ptr(), qs.data(), grad_q.data_ptr(), dqs.data(), dq_code, ch.k.data(), ch.v.data(), ks.data(),
       ch.dk.data(), ch.dv.data(), dks.data(), dkv_code, ch.chunk_len, lens, grad_out.data_ptr(), gs.data(),
       m_i.data_ptr(), m_code, l_i.data_ptr<float>(), D.data_ptr<float>(), B, H, T, Dh, static_cast<int>(sp_size),
-      static_cast<int>(ring_rank), static_cast<float>(scale), ws.data_ptr(), ws_bytes, stream);
+      static_cast<int>(ring_rank), static_cast<float>(scale), ws_ptr(ws), ws_bytes, stream);
   check_status(rc, "ring_attention_backward");
   return std::make_tuple(grad_q, dK, dV);
 }

@@ -99,14 +99,31 @@ def _lens_arg(kv_lens):
     return None if kv_lens is None else _lib.i32_array(kv_lens)
 
 
+_SIZE_MAX = 2**64 - 1
+
+
 def forward_workspace_bytes(B, H, D, sp_size, chunk_len, kv_lens=None) -> int:
-    return int(_lib.load_abi().harp_ra_forward_workspace_bytes(B, H, D, sp_size, chunk_len, _lens_arg(kv_lens)))
+    """Device scratch bytes the forward needs (raises on invalid sizes)."""
+    n = int(_lib.load_abi().harp_ra_forward_workspace_bytes(B, H, D, sp_size, chunk_len, _lens_arg(kv_lens)))
+    if n == _SIZE_MAX:
+        raise ValueError(_lib.last_error())
+    return n
 
 
 def backward_workspace_bytes(B, H, T, D, sp_size, chunk_len, kv_lens=None) -> int:
-    return int(
-        _lib.load_abi().harp_ra_backward_workspace_bytes(B, H, T, D, sp_size, chunk_len, _lens_arg(kv_lens))
-    )
+    """Device scratch bytes the backward needs (raises on invalid sizes)."""
+    n = int(_lib.load_abi().harp_ra_backward_workspace_bytes(B, H, T, D, sp_size, chunk_len, _lens_arg(kv_lens)))
+    if n == _SIZE_MAX:
+        raise ValueError(_lib.last_error())
+    return n
+
+
+def _workspace(nbytes: int, device) -> torch.Tensor:
+    return torch.empty(nbytes, dtype=torch.uint8, device=device)
+
+
+def _ws_ptr(ws: torch.Tensor):
+    return ws.data_ptr() if ws.numel() else None
 
 
 def abi_forward(
@@ -127,8 +144,7 @@ def abi_forward(
     n = len(k_chunks)
     chunk_len = k_chunks[0].shape[2]
     if workspace is None:
-        workspace = torch.empty(forward_workspace_bytes(B, H, D, n, chunk_len, kv_lens), dtype=torch.uint8,
-                                device=q.device)
+        workspace = _workspace(forward_workspace_bytes(B, H, D, n, chunk_len, kv_lens), q.device)
     m_code = _lib.HARP_RA_BF16 if m_i.dtype == torch.bfloat16 else _lib.HARP_RA_F32
     rc = lib.harp_ra_forward(
         q.data_ptr(), _strides(q),
@@ -136,7 +152,7 @@ def abi_forward(
         _strides(k_chunks[0]), chunk_len, _lens_arg(kv_lens),
         out.data_ptr(), _strides(out), m_i.data_ptr(), m_code, l_i.data_ptr(),
         B, H, T, D, n, ring_rank, float(scale),
-        workspace.data_ptr(), workspace.numel(), _stream_ptr(stream),
+        _ws_ptr(workspace), workspace.numel(), _stream_ptr(stream),
     )
     _lib.check(rc, "harp_ra_forward")
 
@@ -171,8 +187,7 @@ def abi_backward(
     n = len(k_chunks)
     chunk_len = k_chunks[0].shape[2]
     if workspace is None:
-        workspace = torch.empty(backward_workspace_bytes(B, H, T, D, n, chunk_len, kv_lens), dtype=torch.uint8,
-                                device=q.device)
+        workspace = _workspace(backward_workspace_bytes(B, H, T, D, n, chunk_len, kv_lens), q.device)
 
     def code(t):
         return _lib.HARP_RA_BF16 if t.dtype == torch.bfloat16 else _lib.HARP_RA_F32
@@ -187,7 +202,7 @@ def abi_backward(
         grad_out.data_ptr(), _strides(grad_out),
         m_i.data_ptr(), code(m_i), l_i.data_ptr(), delta.data_ptr(),
         B, H, T, D, n, ring_rank, float(scale),
-        workspace.data_ptr(), workspace.numel(), _stream_ptr(stream),
+        _ws_ptr(workspace), workspace.numel(), _stream_ptr(stream),
     )
     _lib.check(rc, "harp_ra_backward")
 

@@ -109,8 +109,9 @@ HARP_RA_API int harp_ra_delta(const void* grad_out, const int64_t* do_strides,
                   int batch, int h_num, int t_num, int h_len, void* stream);
 
 /*
- * Device workspace the forward / backward need for these sizes (0 when the
- * arguments are invalid).  Replaces the reference's grow-only scratch sizing
+ * Device workspace the forward / backward need for these sizes ((size_t)-1
+ * when the arguments are invalid; 0 = none needed, the current kernels keep
+ * all staging in LDS).  Replaces the reference's grow-only scratch sizing
  * (RingAttnHbmWorkspace::ensure_slot, ring_attn.cpp:620-840, sized at
  * :2428-2450 and :2595-2656).
  */
@@ -134,7 +135,7 @@ HARP_RA_API const char* harp_ra_last_error(void);
  * last read, then clears them.  Not thread-safe with concurrent calls.
  */
 enum {
-  HARP_RA_KERNEL_PACK = 0,
+  HARP_RA_KERNEL_PACK = 0, /* reserved: operand repacking (unused by the current kernels) */
   HARP_RA_KERNEL_FWD = 1,
   HARP_RA_KERNEL_DELTA = 2,
   HARP_RA_KERNEL_DKDV = 3,

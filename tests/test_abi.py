@@ -76,7 +76,7 @@ def _fwd_call(**over):
         (dict(lens=_lib.i32_array([129])), _lib.HARP_RA_EINVAL, "kv_valid_lens"),
         (dict(mdt=7), _lib.HARP_RA_EINVAL, "m_i_dtype"),
         (dict(scale=float("nan")), _lib.HARP_RA_EINVAL, "scale"),
-        (dict(wsb=16), _lib.HARP_RA_ENOMEM, "workspace"),
+        (dict(scale=-0.125), _lib.HARP_RA_EINVAL, "positive"),
     ],
 )
 def test_forward_rejects_bad_arguments_before_any_device_call(over, code, msg):
@@ -86,14 +86,14 @@ def test_forward_rejects_bad_arguments_before_any_device_call(over, code, msg):
 
 
 def test_workspace_sizes():
-    fwd = harp_amd.forward_workspace_bytes(1, 24, 128, 8, 8192)
-    assert fwd == 1 * 24 * 128 * 8 * 8192 * 2
-    bwd = harp_amd.backward_workspace_bytes(1, 24, 8192, 128, 8, 8192)
-    assert bwd == 24 * 128 * 65536 * 2 + 2 * 24 * 128 * 8192 * 2
-    # D=72 pads panels to 96 rows; ragged chunk lengths round up to 64 keys
-    assert harp_amd.forward_workspace_bytes(2, 16, 72, 4, 4480, [4429] * 4) == 2 * 16 * 96 * 4 * 4480 * 2
-    assert harp_amd.forward_workspace_bytes(1, 1, 64, 0, 64) == 0
-    assert harp_amd.forward_workspace_bytes(1, 1, 66, 1, 64) == 0
+    # all staging lives in LDS: no device scratch for valid sizes
+    assert harp_amd.forward_workspace_bytes(1, 24, 128, 8, 8192) == 0
+    assert harp_amd.backward_workspace_bytes(1, 24, 8192, 128, 8, 8192) == 0
+    assert harp_amd.forward_workspace_bytes(2, 16, 72, 4, 4480, [4429] * 4) == 0
+    with pytest.raises(ValueError, match="sp_size"):
+        harp_amd.forward_workspace_bytes(1, 1, 64, 0, 64)
+    with pytest.raises(ValueError, match="multiple of 8"):
+        harp_amd.forward_workspace_bytes(1, 1, 66, 1, 64)
 
 
 def test_timing_read_validates_arguments():

@@ -10,6 +10,7 @@ sum over keys of dV equals sum over queries of dO, sum over keys of dK is 0.
 """
 
 import math
+import os
 
 import numpy as np
 import pytest
@@ -47,8 +48,15 @@ def _oracle_full(q, ks, vs, do, scale, rank=0, lens=None, dtype=torch.float64):
 
 def _report(name, got, ref, tol):
     r = rel_fro(got, ref)
-    print(f"  {name}: rel_fro={r:.3e} rel_max={rel_max(got, ref):.3e} (tol {tol})", flush=True)
-    assert math.isfinite(r) and r <= tol, f"{name} rel error {r:.3e} > {tol}"
+    rm = rel_max(got, ref)
+    line = f"  {name}: rel_fro={r:.3e} rel_max={rm:.3e} (tol {tol})"
+    print(line, flush=True)
+    log = os.environ.get("HARP_PARITY_LOG")
+    if log:
+        with open(log, "a") as f:
+            f.write(f"{os.environ.get('PYTEST_CURRENT_TEST', '').split(' ')[0]} {line.strip()}\n")
+    ok = math.isfinite(r) and r <= tol
+    assert ok, f"{name} rel error {r:.3e} > {tol}"
 
 
 def _check_all(res, ref, valid_key_mask=None):
@@ -206,28 +214,35 @@ def test_layouts_dtypes_and_paths_agree():
     for kw in variants:
         print(f"  variant {kw}", flush=True)
         r = run_hip(q, ks, vs, do, scale, **kw)
-        assert torch.equal(r["o"], base["o"]), kw
-        assert (r["lse"] - base["lse"]).abs().max() < 1e-5, kw
+        same_o = torch.equal(r["o"], base["o"])
+        lse_diff = (r["lse"] - base["lse"]).abs().max().item()
+        assert same_o and lse_diff < 1e-5, (kw, same_o, lse_diff)
         if "grad_dtype" in kw:
             _check_all(r, ref)
         elif "m_dtype" in kw:
             # fp32 m changes P's rounding only
             for key in ("dq", "dk", "dv"):
-                assert rel_fro(r[key], base[key]) < 1e-2, key
+                err = rel_fro(r[key], base[key])
+                assert err < 1e-2, (key, err)
         else:
             for key in ("dq", "dk", "dv", "delta"):
-                assert torch.equal(r[key], base[key]), (kw, key)
+                same = torch.equal(r[key], base[key])
+                assert same, (kw, key)
 
 
 @pytest.mark.parametrize("rank", [1, 2])
 def test_ring_rank_order(rank):
+    """ring_rank changes the chunk visiting order; the result stays within the
+    bar of the oracle, and differs from rank 0 only by bf16 rounding of P
+    (the running max, the reference point of P, is reached in another order)."""
     q, ks, vs, do, scale = _small()
+    ref = _oracle_full(q, ks, vs, do, scale, rank=rank)
     base = run_hip(q, ks, vs, do, scale)
     r = run_hip(q, ks, vs, do, scale, ring_rank=rank)
-    assert rel_fro(r["o"], base["o"]) < 1e-5
-    assert (r["lse"] - base["lse"]).abs().max() < 1e-4
-    for key in ("dq", "dk", "dv"):
-        assert rel_fro(r[key], base[key]) < 1e-2
+    _check_all(r, ref)
+    err_o = rel_fro(r["o"], base["o"])
+    err_lse = (r["lse"] - base["lse"]).abs().max().item()
+    assert err_o < 5e-3 and err_lse < 1e-4, (err_o, err_lse)
 
 
 def test_bf16_m_is_lse_consistent():
