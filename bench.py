@@ -130,6 +130,9 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=3407)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU-baseline sample time")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="before the timed steps, run one plain device copy of this many MiB "
+                         "(a known-size reference for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -165,6 +168,15 @@ def main() -> int:
         ops.ring_attention_forward(q, k, v, out, m_i, l_i, N, scale, 0, lens)
         delta = ops.ring_attention_delta(do, out)
         ops.ring_attention_backward(q, dq, k, dk, v, dv, do, m_i, l_i, delta, N, scale, 0, lens)
+
+    if args.copy_calibration_mib > 0:
+        n = args.copy_calibration_mib * (1 << 20) // 4
+        src = torch.ones(n, device=dev, dtype=torch.float32)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     for _ in range(args.warmup):
         step()

@@ -72,6 +72,16 @@ int check_plain_view(const void* p, const int64_t* s, const char* name) {
   return HARP_RA_OK;
 }
 
+// Streamed operands are read through 32-bit buffer offsets: every [rows][D]
+// view the kernels walk (one (b, h) of a chunk, of q or of grad_out) must
+// span less than 2^31 bytes.
+int check_extent(int rows, const int64_t* s, const char* name) {
+  if ((int64_t)rows * s[2] * 2 >= ((int64_t)1 << 31))
+    return fail(HARP_RA_EUNSUPPORTED, "%s: %d rows x row stride %lld elements exceeds the 2 GiB buffer range", name,
+                rows, (long long)s[2]);
+  return HARP_RA_OK;
+}
+
 int check_dims(int batch, int h_num, int t_num, int h_len) {
   if (batch < 1 || h_num < 1 || t_num < 1 || h_len < 1)
     return fail(HARP_RA_EINVAL, "sizes must be positive (B=%d H=%d T=%d D=%d)", batch, h_num, t_num, h_len);
@@ -270,6 +280,7 @@ int harp_ra_forward(const void* q, const int64_t* q_strides, const void* const* 
     if ((rc = check_bf16_view(v_chunks[c], kv_strides, "v chunk"))) return rc;
   }
   if ((rc = check_plain_view(out, out_strides, "out"))) return rc;
+  if ((rc = check_extent(kv_chunk_len, kv_strides, "k/v chunk"))) return rc;
   if (!m_i || !l_i) return fail(HARP_RA_EINVAL, "m_i / l_i are NULL");
   if (m_i_dtype != HARP_RA_F32 && m_i_dtype != HARP_RA_BF16) return fail(HARP_RA_EINVAL, "m_i_dtype must be F32 or BF16");
 
@@ -367,6 +378,9 @@ int harp_ra_backward(const void* q, const int64_t* q_strides, void* grad_q, cons
     if ((rc = check_plain_view(dk_chunks[c], dkv_strides, "dK chunk"))) return rc;
     if ((rc = check_plain_view(dv_chunks[c], dkv_strides, "dV chunk"))) return rc;
   }
+  if ((rc = check_extent(kv_chunk_len, kv_strides, "k/v chunk"))) return rc;
+  if ((rc = check_extent(t_num, q_strides, "q"))) return rc;
+  if ((rc = check_extent(t_num, do_strides, "grad_out"))) return rc;
   if (!m_i || !l_i || !delta) return fail(HARP_RA_EINVAL, "m_i / l_i / delta are NULL");
   if (m_i_dtype != HARP_RA_F32 && m_i_dtype != HARP_RA_BF16) return fail(HARP_RA_EINVAL, "m_i_dtype must be F32 or BF16");
 
