@@ -13,17 +13,13 @@
 //   dkdv_kernel   per 128-key tile (KV-stationary like the reference): per 64-query
 //                 tile recompute S, dP; dV += P^T dO, dK += dS^T Q.
 //
-// Memory path: every streamed 64-row tile is fetched with buffer loads (the
-// hardware range check zero-fills rows past a chunk's valid length and
-// columns past D), staged in registers while the current tile computes, and
-// written to one of two LDS buffers (one barrier per tile).  LDS rows are
-// stored with an XOR swizzle of their 16-byte chunks, chunk c of row r at
-// position c ^ swz(r), which keeps both access patterns below free of bank
-// conflicts:
-//   * row reads (ds_read_b128, MFMA operand rows: 8 consecutive rows, one
-//     chunk) and
-//   * transposed reads (ds_read_b64_tr_b16, MFMA operands that need the tile
-//     transposed: V^T, K^T, dO^T, Q^T — 4 rows x 2 chunks per 16 lanes).
+// Memory path: every streamed 64-row tile is copied global -> LDS by
+// buffer_load_dwordx4 ... lds (no register staging).  The buffer range check
+// zero-fills rows past a chunk's valid length and columns past D.  Two LDS
+// buffers alternate: after the barrier that publishes tile t, the loads of
+// tile t+1 go into the buffer every wave has finished reading, and overlap
+// the MFMA work on tile t.  Within each MFMA phase the LDS operand fragments
+// are issued two steps ahead of the MFMAs that consume them.
 // Accumulation is fp32 in registers; P and dS are rounded to bf16 only as
 // MFMA operands; exp is v_exp_f32 (exp2) with log2(e) folded into the scale.
 #include "ra_common.h"
@@ -32,101 +28,142 @@
 namespace harp_ra {
 
 typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+typedef __attribute__((address_space(3))) void lds_void;
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 
 constexpr uint32_t kOOB = 0x80000000u;  // buffer offset past every valid range: loads 0
 
-__device__ __forceinline__ int swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+// LDS is 64 banks x 4 bytes (256 bytes per cycle); 16-byte accesses are
+// served 16 lanes per cycle, 8-byte accesses 32 lanes per cycle.  Two tile
+// layouts, both free of bank conflicts for the accesses they get:
+//  * PadTile (tiles read only as MFMA row fragments): rows padded to DP+8
+//    elements, so 16 consecutive rows start 16 bytes apart modulo 256 and a
+//    16-row x one-chunk ds_read_b128 touches every bank once; every fragment
+//    offset is a per-lane base plus an immediate.
+//  * XorTile (tiles also read transposed): 256-byte rows, chunk c of row r at
+//    position c ^ swz(r) with swz(r) = 4*(r%4) + (r/4)%4, a permutation over
+//    any 16 rows.  Row reads (16 rows x one chunk) and ds_read_b64_tr_b16
+//    (rows r0+4g+{0..3} x chunks 4db+{0..3} -> positions
+//    4*(db ^ (r%4)) + ((c%4) ^ ((r/4)%4))) hit distinct banks.
+// Both are written by direct-to-LDS loads: one wave instruction fills 64
+// consecutive 16-byte slots; slot() maps a slot to its (row, chunk).
+__device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 
-// 64-row LDS tile of DP (>= D) bf16 columns, row width W, swizzled chunks.
 template <int DP>
-struct Tile {
-  static constexpr int W = DP <= 64 ? 64 : 128;
+struct XorTile {
+  static constexpr int W = 128;
   static constexpr int NCH = DP / 8;  // 16-byte data chunks per row
   static constexpr int ELEMS = 64 * W;
-  static __device__ __forceinline__ int off(int r, int c) { return r * W + ((c ^ swz(r)) << 3); }
+  static constexpr int SLOTS = ELEMS / 8;
+  static __device__ __forceinline__ void slot(int s, int& r, int& c) {
+    r = s >> 4;
+    c = (s & 15) ^ swz(r);
+  }
+};
+
+template <int DP>
+struct PadTile {
+  static constexpr int W = DP + 8;
+  static constexpr int NCH = DP / 8;
+  static constexpr int SPR = W / 8;  // slots per row (the last one is padding)
+  static constexpr int ELEMS = 64 * W;
+  static constexpr int SLOTS = ELEMS / 8;
+  static __device__ __forceinline__ void slot(int s, int& r, int& c) {
+    r = s / SPR;
+    c = s % SPR;
+  }
 };
 
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
-__device__ __forceinline__ bf16x8 buf_load16(rsrc_t r, uint32_t voff) {
-  return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0));
-}
-
-// Per-thread share of a 64-row tile: which 16-byte chunks this thread moves
-// (byte offsets relative to the tile's first row, and LDS element offsets).
-template <int DP, int NTHR>
-struct TileMap {
-  using G = Tile<DP>;
-  static constexpr int kTot = 64 * G::NCH;
-  static constexpr int kN = (kTot + NTHR - 1) / NTHR;
-  uint32_t voff[kN];
-  int loff[kN];
-  __device__ __forceinline__ void init(int64_t row_stride, int D, int tid) {
-#pragma unroll
-    for (int i = 0; i < kN; ++i) {
-      const int idx = tid + i * NTHR;
-      const int r = idx / G::NCH, c = idx % G::NCH;
-      const bool in_tile = (kTot % NTHR == 0) || idx < kTot;
-      voff[i] = (in_tile && c * 8 < D) ? (uint32_t)(r * row_stride * 2 + c * 16) : kOOB;
-      loff[i] = in_tile ? G::off(r, c) : -1;
-    }
-  }
-};
-
-template <int DP, int NTHR>
-struct TileRegs {
-  using M = TileMap<DP, NTHR>;
-  bf16x8 v[M::kN];
-  __device__ __forceinline__ void load(const M& m, rsrc_t r) {
-#pragma unroll
-    for (int i = 0; i < M::kN; ++i) v[i] = buf_load16(r, m.voff[i]);
-  }
-  __device__ __forceinline__ void store(const M& m, bf16* lds) const {
-#pragma unroll
-    for (int i = 0; i < M::kN; ++i)
-      if ((M::kTot % NTHR == 0) || m.loff[i] >= 0) *(bf16x8*)(lds + m.loff[i]) = v[i];
-  }
-};
 
 // Buffer resource over rows [row0, row0 + rows) of a [rows][stride] bf16 view.
 __device__ __forceinline__ rsrc_t rows_rsrc(const bf16* base, int64_t stride, int row0, int rows) {
   return make_rsrc(base + (int64_t)row0 * stride, (uint32_t)((int64_t)(rows > 0 ? rows : 0) * stride * 2));
 }
 
-// Lane offsets for the two LDS read patterns of a Tile<DP>.
-template <int DP>
-struct LaneOffsets {
-  using G = Tile<DP>;
-  static constexpr int NDB = DP / 32;
-  // row reads: row = rb*32 + l32, chunk = 2*ks + g  ->  rb*32*W + row_off[ks&3] + (ks>>2)*64
-  int row_off[4];
-  // transposed reads: rows r0 + 4g + s (+8), columns c0 + l32 with c0 = 32*db
-  //   ->  r0*W + tr_off[db]  (second half: + 8*W)
-  int tr_off[NDB];
-  __device__ __forceinline__ void init(int lane) {
-    const int l32 = lane & 31, g = lane >> 5;
-    const int y = g ^ swz(l32);
+// This wave's share of the direct-to-LDS copies of one 64-row tile: slot
+// instruction i (64 slots) goes to waves round-robin; voff holds each lane's
+// byte offset (relative to the tile's first row) or kOOB for padding slots
+// and columns past D, which the range check turns into zeros.
+template <class G, int NW>
+struct DirectLoader {
+  static constexpr int kInstTot = G::SLOTS / 64;
+  static constexpr int kInst = (kInstTot + NW - 1) / NW;
+  uint32_t voff[kInst];
+  int wave;
+  __device__ __forceinline__ void init(int64_t row_stride, int D, int wave_, int lane) {
+    wave = wave_;
 #pragma unroll
-    for (int b = 0; b < 4; ++b) row_off[b] = l32 * G::W + (((2 * b) ^ y) << 3);
+    for (int k = 0; k < kInst; ++k) {
+      const int inst = wave + k * NW;
+      int r, c;
+      G::slot(inst * 64 + lane, r, c);
+      const bool ok = inst < kInstTot && c < G::NCH && c * 8 < D;
+      voff[k] = ok ? (uint32_t)(r * row_stride * 2 + c * 16) : kOOB;
+    }
+  }
+  __device__ __forceinline__ void load(rsrc_t rs, bf16* tile) const {
+#pragma unroll
+    for (int k = 0; k < kInst; ++k) {
+      const int inst = wave + k * NW;
+      if (kInstTot % NW == 0 || inst < kInstTot)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(tile + inst * 512), 16, voff[k], 0, 0, 0);
+    }
+  }
+};
+
+// Wait for this thread's direct-to-LDS loads (a barrier then publishes them).
+__device__ __forceinline__ void wait_lds_loads() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Row fragment T[rb*32 + l32][16*ks + 8*g .. +7] of a PadTile: per-lane base,
+// immediate per (rb, ks).
+template <int DP>
+struct PadRows {
+  using G = PadTile<DP>;
+  int base;
+  __device__ __forceinline__ void init(int lane) { base = (lane & 31) * G::W + 8 * (lane >> 5); }
+  __device__ __forceinline__ bf16x8 frag(const bf16* t, int rb, int ks) const {
+    return *(const bf16x8*)(t + base + rb * 32 * G::W + ks * 16);
+  }
+};
+
+// Lane offsets for the two read patterns of an XorTile.
+template <int DP, int KSTEPS>
+struct XorLanes {
+  using G = XorTile<DP>;
+  static constexpr int NDB = DP / 32;
+  // row reads: T[rb*32 + l32][16*ks + 8*g .. +7] at rb*32*W + row_off[ks]
+  int row_off[KSTEPS];
+  // transposed reads: rows r0 + 8*hh + 4g + s, columns 32*db + l32 (r0 % 16 == 0)
+  //   at r0*W + tr_off[hh][db]
+  int tr_off[2][NDB];
+  __device__ __forceinline__ void init(int lane, bool rows = true) {
+    const int l32 = lane & 31, g = lane >> 5;
+    if (rows) {
+#pragma unroll
+      for (int ks = 0; ks < KSTEPS; ++ks) row_off[ks] = l32 * G::W + (((2 * ks + g) ^ swz(l32)) << 3);
+    }
     const int j = lane >> 4, s = (lane >> 2) & 3, m = lane & 3;
-    const int row = 4 * g + s;
     const int cl = 2 * (j & 1) + (m >> 1);
 #pragma unroll
-    for (int db = 0; db < NDB; ++db) tr_off[db] = row * G::W + (((4 * db + cl) ^ swz(row)) << 3) + 4 * (m & 1);
+    for (int hh = 0; hh < 2; ++hh) {
+      const int row = 8 * hh + 4 * g + s;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+        tr_off[hh][db] = row * G::W + (((4 * db + cl) ^ swz(row)) << 3) + 4 * (m & 1);
+    }
   }
-  // A/B operand row fragment: T[rb*32 + l32][16*ks + 8*g .. +7]
   __device__ __forceinline__ bf16x8 row_frag(const bf16* t, int rb, int ks) const {
-    return *(const bf16x8*)(t + rb * 32 * G::W + row_off[ks & 3] + (ks >> 2) * 64);
+    return *(const bf16x8*)(t + rb * 32 * G::W + row_off[ks]);
   }
   // k-operand fragment read transposed: T[r0 + {4g+0..3, 8+4g+0..3}][32*db + l32]
   // ds_read_b64_tr_b16: in each 16-lane group, lane i slot s' receives element
   // i%4 of the 8 bytes addressed by lane 4s' + i/4 of that group.
   __device__ __forceinline__ bf16x8 tr_frag(const bf16* t, int r0, int db) const {
-    const bf16* p0 = t + r0 * G::W + tr_off[db];
-    const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p0);
-    const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p0 + 8 * G::W));
+    const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(t + r0 * G::W + tr_off[0][db]));
+    const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(t + r0 * G::W + tr_off[1][db]));
     bf16x8 r;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -138,10 +175,36 @@ struct LaneOffsets {
 };
 
 // Register-class pins (emit no instructions): long-lived MFMA accumulators
-// stay in AGPRs, values the VALU consumes stay in VGPRs, so the allocator does
-// not shuttle them between the two files inside the main loops.
+// and block-constant operands stay in AGPRs, so the allocator neither
+// shuttles them between register files inside the loops nor crowds the VGPRs.
 __device__ __forceinline__ void pin_agpr(f32x16& x) { asm volatile("" : "+a"(x)); }
-__device__ __forceinline__ void pin_vgpr(f32x16& x) { asm volatile("" : "+v"(x)); }
+__device__ __forceinline__ void pin_agpr(bf16x8& x) { asm volatile("" : "+a"(x)); }
+
+// Scheduling fence: the compiler may not move any instruction across it.
+__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
+
+// N MFMA steps whose LDS operand fragments are issued PF steps ahead:
+// load(i) returns step i's fragments, mma(i, frags) issues its MFMAs.  The
+// fences keep each step's reads above the MFMAs of the earlier steps, so the
+// s_waitcnt before an MFMA leaves the later reads in flight.
+template <int N, int PF, class Load, class Mma>
+__device__ __forceinline__ void pipelined(const Load& load, const Mma& mma) {
+  using F = decltype(load(0));
+  F f[PF + 1];
+#pragma unroll
+  for (int i = 0; i < PF && i < N; ++i) f[i] = load(i);
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    if (i + PF < N) f[(i + PF) % (PF + 1)] = load(i + PF);
+    sched_fence();
+    mma(i, f[i % (PF + 1)]);
+    sched_fence();
+  }
+}
+
+struct Frag2 {
+  bf16x8 a, b;
+};
 
 __device__ __forceinline__ float wave_half_max(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -184,10 +247,11 @@ __device__ __forceinline__ void next_tile(const ChunkTable& ct, int step, int k0
 template <int KSTEPS, int DBLK>
 __global__ __launch_bounds__(256, 2) void fwd_kernel(FwdParams p) {
   constexpr int DP = DBLK * 32;
-  using G = Tile<DP>;
+  using GK = PadTile<DP>;  // K: row fragments only
+  using GV = XorTile<DP>;  // V: transposed fragments
   constexpr float kTau = 8.f;  // lazy-rescale threshold (log2 units): P <= 2^8
-  __shared__ __attribute__((aligned(16))) bf16 Ks[2][G::ELEMS];
-  __shared__ __attribute__((aligned(16))) bf16 Vs[2][G::ELEMS];
+  __shared__ __attribute__((aligned(16))) bf16 Ks[2][GK::ELEMS];
+  __shared__ __attribute__((aligned(16))) bf16 Vs[2][GV::ELEMS];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, g = lane >> 5;
@@ -206,10 +270,14 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(FwdParams p) {
       qf[ks] = (q_ok && d0 < p.D) ? *(const bf16x8*)(qrow + d0) : zero8();
     }
   }
-  LaneOffsets<DP> lo;
-  lo.init(lane);
-  TileMap<DP, 256> tm;
-  tm.init(p.skt, p.D, tid);
+  PadRows<DP> klo;
+  klo.init(lane);
+  XorLanes<DP, KSTEPS> vlo;
+  vlo.init(lane, false);
+  DirectLoader<GK, 4> kld;
+  kld.init(p.skt, p.D, wave, lane);
+  DirectLoader<GV, 4> vld;
+  vld.init(p.skt, p.D, wave, lane);
 
   f32x16 o[DBLK];
 #pragma unroll
@@ -219,41 +287,33 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(FwdParams p) {
   float l_run = 0.f;        // this lane-half's partial sum of exp2(s*c2 - m_ref)
 
   const int64_t kvo = (int64_t)b * p.skb + (int64_t)h * p.skh;
+  auto issue = [&](int step, int k0, int bf) {
+    const int c = p.ct.order[step];
+    const int rows = p.ct.len[c] - k0;
+    kld.load(rows_rsrc(p.ct.k[c] + kvo, p.skt, k0, rows), Ks[bf]);
+    vld.load(rows_rsrc(p.ct.v[c] + kvo, p.skt, k0, rows), Vs[bf]);
+  };
   int step = 0, k0 = 0;
   while (step < p.ct.n && p.ct.len[p.ct.order[step]] == 0) ++step;
-  TileRegs<DP, 256> kr, vr;
   int buf = 0;
-  if (step < p.ct.n) {
-    const int c = p.ct.order[step];
-    kr.load(tm, rows_rsrc(p.ct.k[c] + kvo, p.skt, 0, p.ct.len[c]));
-    vr.load(tm, rows_rsrc(p.ct.v[c] + kvo, p.skt, 0, p.ct.len[c]));
-    kr.store(tm, Ks[0]);
-    vr.store(tm, Vs[0]);
-  }
+  if (step < p.ct.n) issue(step, 0, 0);
 #pragma unroll 1
   while (step < p.ct.n) {
     const int kv_left = p.ct.len[p.ct.order[step]] - k0;
     int nstep, nk0;
     next_tile(p.ct, step, k0, nstep, nk0);
-    const bool has_next = nstep < p.ct.n;
-    if (has_next) {
-      const int c = p.ct.order[nstep];
-      const int rows = p.ct.len[c] - nk0;
-      kr.load(tm, rows_rsrc(p.ct.k[c] + kvo, p.skt, nk0, rows));
-      vr.load(tm, rows_rsrc(p.ct.v[c] + kvo, p.skt, nk0, rows));
-    }
+    wait_lds_loads();
     __syncthreads();
+    if (nstep < p.ct.n) issue(nstep, nk0, buf ^ 1);
     const bf16* K = Ks[buf];
     const bf16* V = Vs[buf];
 
-    // S^T (keys x queries), two 32-key blocks
+    // S^T (keys x queries), two 32-key blocks; step i = (ks = i/2, kb = i%2)
     f32x16 s[2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) s[kb] = zero16();
-#pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks)
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) s[kb] = mfma32x32x16(lo.row_frag(K, kb, ks), qf[ks], s[kb]);
+    s[0] = zero16();
+    s[1] = zero16();
+    pipelined<2 * KSTEPS, 2>([&](int i) { return klo.frag(K, i & 1, i >> 1); },
+                             [&](int i, const bf16x8& a) { s[i & 1] = mfma32x32x16(a, qf[i >> 1], s[i & 1]); });
     if (kv_left < 64) {  // tail tile of a chunk: mask keys past its valid length
       // a side-effecting (empty) asm keeps this a real uniform branch instead
       // of selects that would run on every tile
@@ -297,15 +357,12 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(FwdParams p) {
           pf[kb * 2 + hf][j] = (bf16)e;
         }
 
-    // O^T += V^T P^T
-#pragma unroll
-    for (int ks2 = 0; ks2 < 4; ++ks2)
-#pragma unroll
-      for (int db = 0; db < DBLK; ++db) o[db] = mfma32x32x16(lo.tr_frag(V, ks2 * 16, db), pf[ks2], o[db]);
+    // O^T += V^T P^T; step i = (ks2 = i / DBLK, db = i % DBLK)
+    pipelined<4 * DBLK, 2>([&](int i) { return vlo.tr_frag(V, (i / DBLK) * 16, i % DBLK); },
+                           [&](int i, const bf16x8& a) {
+                             o[i % DBLK] = mfma32x32x16(a, pf[i / DBLK], o[i % DBLK]);
+                           });
 
-    if (!has_next) break;
-    kr.store(tm, Ks[buf ^ 1]);
-    vr.store(tm, Vs[buf ^ 1]);
     buf ^= 1;
     step = nstep;
     k0 = nk0;
@@ -382,9 +439,10 @@ __device__ __forceinline__ float lse2_of(const void* m, int m_bf16, const float*
 template <int KSTEPS, int DBLK>
 __global__ __launch_bounds__(256, 2) void dq_kernel(BwdParams p) {
   constexpr int DP = DBLK * 32;
-  using G = Tile<DP>;
-  __shared__ __attribute__((aligned(16))) bf16 Ks[2][G::ELEMS];
-  __shared__ __attribute__((aligned(16))) bf16 Vs[2][G::ELEMS];
+  using GK = XorTile<DP>;  // K: row and transposed fragments
+  using GV = PadTile<DP>;  // V: row fragments only
+  __shared__ __attribute__((aligned(16))) bf16 Ks[2][GK::ELEMS];
+  __shared__ __attribute__((aligned(16))) bf16 Vs[2][GV::ELEMS];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, g = lane >> 5;
@@ -409,55 +467,53 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(BwdParams p) {
   const int64_t si = ((int64_t)b * p.H + h) * p.T + qi;
   const float lse2 = q_ok ? lse2_of(p.m, p.m_bf16, p.l, si) : INFINITY;
   const float dlt = q_ok ? p.delta[si] : 0.f;
-  LaneOffsets<DP> lo;
-  lo.init(lane);
-  TileMap<DP, 256> tm;
-  tm.init(p.skt, p.D, tid);
+  XorLanes<DP, KSTEPS> klo;
+  klo.init(lane);
+  PadRows<DP> vlo;
+  vlo.init(lane);
+  DirectLoader<GK, 4> kld;
+  kld.init(p.skt, p.D, wave, lane);
+  DirectLoader<GV, 4> vld;
+  vld.init(p.skt, p.D, wave, lane);
 
   f32x16 dq[DBLK];
 #pragma unroll
   for (int i = 0; i < DBLK; ++i) dq[i] = zero16();
 
   const int64_t kvo = (int64_t)b * p.skb + (int64_t)h * p.skh;
+  auto issue = [&](int step, int k0, int bf) {
+    const int c = p.ct.order[step];
+    const int rows = p.ct.len[c] - k0;
+    kld.load(rows_rsrc(p.ct.k[c] + kvo, p.skt, k0, rows), Ks[bf]);
+    vld.load(rows_rsrc(p.ct.v[c] + kvo, p.skt, k0, rows), Vs[bf]);
+  };
   int step = 0, k0 = 0;
   while (step < p.ct.n && p.ct.len[p.ct.order[step]] == 0) ++step;
-  TileRegs<DP, 256> kr, vr;
   int buf = 0;
-  if (step < p.ct.n) {
-    const int c = p.ct.order[step];
-    kr.load(tm, rows_rsrc(p.ct.k[c] + kvo, p.skt, 0, p.ct.len[c]));
-    vr.load(tm, rows_rsrc(p.ct.v[c] + kvo, p.skt, 0, p.ct.len[c]));
-    kr.store(tm, Ks[0]);
-    vr.store(tm, Vs[0]);
-  }
+  if (step < p.ct.n) issue(step, 0, 0);
 #pragma unroll 1
   while (step < p.ct.n) {
     int nstep, nk0;
     next_tile(p.ct, step, k0, nstep, nk0);
-    const bool has_next = nstep < p.ct.n;
-    if (has_next) {
-      const int c = p.ct.order[nstep];
-      const int rows = p.ct.len[c] - nk0;
-      kr.load(tm, rows_rsrc(p.ct.k[c] + kvo, p.skt, nk0, rows));
-      vr.load(tm, rows_rsrc(p.ct.v[c] + kvo, p.skt, nk0, rows));
-    }
+    wait_lds_loads();
     __syncthreads();
+    if (nstep < p.ct.n) issue(nstep, nk0, buf ^ 1);
     const bf16* K = Ks[buf];
     const bf16* V = Vs[buf];
 
+    // S^T = K Q^T and dP^T = V dO^T; step i = (ks = i/2, kb = i%2)
     f32x16 s[2], dp[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       s[kb] = zero16();
       dp[kb] = zero16();
     }
-#pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks)
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        s[kb] = mfma32x32x16(lo.row_frag(K, kb, ks), qf[ks], s[kb]);
-        dp[kb] = mfma32x32x16(lo.row_frag(V, kb, ks), gf[ks], dp[kb]);
-      }
+    pipelined<2 * KSTEPS, 2>(
+        [&](int i) { return Frag2{klo.row_frag(K, i & 1, i >> 1), vlo.frag(V, i & 1, i >> 1)}; },
+        [&](int i, const Frag2& f) {
+          s[i & 1] = mfma32x32x16(f.a, qf[i >> 1], s[i & 1]);
+          dp[i & 1] = mfma32x32x16(f.b, gf[i >> 1], dp[i & 1]);
+        });
     bf16x8 dsf[4];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
@@ -467,15 +523,12 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(BwdParams p) {
         dsf[kb * 2 + (r >> 3)][r & 7] = (bf16)(pv * (dp[kb][r] - dlt));
       }
 
-    // dQ^T += K^T dS^T
-#pragma unroll
-    for (int ks2 = 0; ks2 < 4; ++ks2)
-#pragma unroll
-      for (int db = 0; db < DBLK; ++db) dq[db] = mfma32x32x16(lo.tr_frag(K, ks2 * 16, db), dsf[ks2], dq[db]);
+    // dQ^T += K^T dS^T; step i = (ks2 = i / DBLK, db = i % DBLK)
+    pipelined<4 * DBLK, 2>([&](int i) { return klo.tr_frag(K, (i / DBLK) * 16, i % DBLK); },
+                           [&](int i, const bf16x8& a) {
+                             dq[i % DBLK] = mfma32x32x16(a, dsf[i / DBLK], dq[i % DBLK]);
+                           });
 
-    if (!has_next) break;
-    kr.store(tm, Ks[buf ^ 1]);
-    vr.store(tm, Vs[buf ^ 1]);
     buf ^= 1;
     step = nstep;
     k0 = nk0;
@@ -499,20 +552,21 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(BwdParams p) {
 // ---------------------------------------------------------------------------
 // Backward dK/dV (KV-stationary, as ring_attn.cpp:2723-2816)
 // ---------------------------------------------------------------------------
-// Block = 4 waves x 32 keys.  The block's 128 K and V rows stay in LDS for the
-// whole kernel (both are MFMA row operands there); the loop streams 64-query
-// tiles of Q / dO (+ LSE, D) through double-buffered LDS and handles each tile
-// as two 32-query halves.  Pad keys (past the chunk's valid length) are
-// written as zero at the end instead of being masked per tile: in this layout
-// a key's P / dS only reach its own dK / dV rows.
+// Block = 4 waves x 32 keys.  The block's 128 K and V rows are copied to LDS
+// once and each wave keeps its 32 rows as MFMA B operands in AGPRs; the loop
+// streams 64-query tiles of Q / dO (+ LSE, D) through double-buffered LDS and
+// handles each tile as two 32-query halves.  Pad keys (past the chunk's valid
+// length) are written as zero at the end instead of being masked per tile:
+// in this layout a key's P / dS only reach its own dK / dV rows.
 template <int KSTEPS, int DBLK>
 __global__ __launch_bounds__(256, 1) void dkdv_kernel(BwdParams p) {
   constexpr int DP = DBLK * 32;
-  using G = Tile<DP>;
-  __shared__ __attribute__((aligned(16))) bf16 Kb[2 * G::ELEMS];  // 128 key rows
-  __shared__ __attribute__((aligned(16))) bf16 Vb[2 * G::ELEMS];
-  __shared__ __attribute__((aligned(16))) bf16 Qs[2][G::ELEMS];
-  __shared__ __attribute__((aligned(16))) bf16 Gs[2][G::ELEMS];
+  using GK = PadTile<DP>;  // the block's K / V rows: row fragments only
+  using GQ = XorTile<DP>;  // Q / dO tiles: row and transposed fragments
+  __shared__ __attribute__((aligned(16))) bf16 Kb[2 * GK::ELEMS];  // 128 key rows
+  __shared__ __attribute__((aligned(16))) bf16 Vb[2 * GK::ELEMS];
+  __shared__ __attribute__((aligned(16))) bf16 Qs[2][GQ::ELEMS];
+  __shared__ __attribute__((aligned(16))) bf16 Gs[2][GQ::ELEMS];
   __shared__ __attribute__((aligned(16))) float Ls[2][64];
   __shared__ __attribute__((aligned(16))) float Dls[2][64];
 
@@ -539,74 +593,83 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(BwdParams p) {
   }
 
   if (kblk0 < len) {  // block has at least one valid key (block-uniform)
-    LaneOffsets<DP> lo;
+    XorLanes<DP, KSTEPS> lo;
     lo.init(lane);
+    bf16x8 kf[KSTEPS], vf[KSTEPS];
     {
-      TileMap<DP, 256> tmk;
-      tmk.init(p.skt, p.D, tid);
+      DirectLoader<GK, 4> kvl;
+      kvl.init(p.skt, p.D, wave, lane);
       const int64_t kvo = (int64_t)b * p.skb + (int64_t)h * p.skh;
-      TileRegs<DP, 256> t;
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
         const int r0 = kblk0 + 64 * half;
-        t.load(tmk, rows_rsrc(p.ct.k[c] + kvo, p.skt, r0, len - r0));
-        t.store(tmk, Kb + half * G::ELEMS);
-        t.load(tmk, rows_rsrc(p.ct.v[c] + kvo, p.skt, r0, len - r0));
-        t.store(tmk, Vb + half * G::ELEMS);
+        kvl.load(rows_rsrc(p.ct.k[c] + kvo, p.skt, r0, len - r0), Kb + half * GK::ELEMS);
+        kvl.load(rows_rsrc(p.ct.v[c] + kvo, p.skt, r0, len - r0), Vb + half * GK::ELEMS);
+      }
+      wait_lds_loads();
+      __syncthreads();
+      // this wave's 32 K / V rows as MFMA B operands, held in AGPRs for the
+      // whole loop (MFMA reads B from AGPRs directly)
+      PadRows<DP> klo;
+      klo.init(lane);
+#pragma unroll
+      for (int ks = 0; ks < KSTEPS; ++ks) {
+        kf[ks] = klo.frag(Kb, wave, ks);
+        vf[ks] = klo.frag(Vb, wave, ks);
+        pin_agpr(kf[ks]);
+        pin_agpr(vf[ks]);
       }
     }
-    TileMap<DP, 256> tmq, tmg;
-    tmq.init(p.sqt, p.D, tid);
-    tmg.init(p.sdt, p.D, tid);
+    DirectLoader<GQ, 4> qld, gld;
+    qld.init(p.sqt, p.D, wave, lane);
+    gld.init(p.sdt, p.D, wave, lane);
     const bf16* qb_ = p.q + (int64_t)b * p.sqb + (int64_t)h * p.sqh;
     const bf16* gb_ = p.dout + (int64_t)b * p.sdb + (int64_t)h * p.sdh;
     const int64_t sbase = ((int64_t)b * p.H + h) * p.T;
 
-    TileRegs<DP, 256> qr, gr;
     float lse_r = INFINITY, dl_r = 0.f;
-    auto load_q = [&](int q0) {
-      qr.load(tmq, rows_rsrc(qb_, p.sqt, q0, p.T - q0));
-      gr.load(tmg, rows_rsrc(gb_, p.sdt, q0, p.T - q0));
+    auto issue = [&](int q0, int bf) {
+      qld.load(rows_rsrc(qb_, p.sqt, q0, p.T - q0), Qs[bf]);
+      gld.load(rows_rsrc(gb_, p.sdt, q0, p.T - q0), Gs[bf]);
       if (tid < 64) {
         const int qq = q0 + tid;
         lse_r = (qq < p.T) ? lse2_of(p.m, p.m_bf16, p.l, sbase + qq) : INFINITY;
         dl_r = (qq < p.T) ? p.delta[sbase + qq] : 0.f;
       }
     };
-    auto store_q = [&](int bf) {
-      qr.store(tmq, Qs[bf]);
-      gr.store(tmg, Gs[bf]);
+    auto store_stats = [&](int bf) {
       if (tid < 64) {
         Ls[bf][tid] = lse_r;
         Dls[bf][tid] = dl_r;
       }
     };
-    load_q(0);
-    store_q(0);
+    issue(0, 0);
+    store_stats(0);
     int buf = 0;
 #pragma unroll 1
     for (int q0 = 0; q0 < p.T; q0 += 64) {
       const bool has_next = q0 + 64 < p.T;
-      if (has_next) load_q(q0 + 64);
+      wait_lds_loads();
       __syncthreads();
+      if (has_next) issue(q0 + 64, buf ^ 1);
       const bf16* Q = Qs[buf];
       const bf16* Gd = Gs[buf];
+
 #pragma unroll
       for (int i = 0; i < DBLK; ++i) {
         pin_agpr(dk[i]);
         pin_agpr(dv[i]);
       }
-
       // per 32-query half: S = Q K^T, dP = dO V^T (C row = query, col = key),
       // then P, dS and the dV / dK updates of that half
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb) {
         f32x16 s = zero16(), dp = zero16();
-#pragma unroll
-        for (int ks = 0; ks < KSTEPS; ++ks) {
-          s = mfma32x32x16(lo.row_frag(Q, qb, ks), lo.row_frag(Kb, wave, ks), s);
-          dp = mfma32x32x16(lo.row_frag(Gd, qb, ks), lo.row_frag(Vb, wave, ks), dp);
-        }
+        pipelined<KSTEPS, 2>([&](int ks) { return Frag2{lo.row_frag(Q, qb, ks), lo.row_frag(Gd, qb, ks)}; },
+                             [&](int ks, const Frag2& f) {
+                               s = mfma32x32x16(f.a, kf[ks], s);
+                               dp = mfma32x32x16(f.b, vf[ks], dp);
+                             });
         bf16x8 pf[2], dsf[2];
 #pragma unroll
         for (int i4 = 0; i4 < 4; ++i4) {
@@ -620,24 +683,27 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(BwdParams p) {
             dsf[r >> 3][r & 7] = (bf16)(pv * (dp[r] - dl4[t]));
           }
         }
-        // dV += P^T dO ; dK += dS^T Q   (M = keys, N = d, K = the 32 queries of this half)
-#pragma unroll
-        for (int h2 = 0; h2 < 2; ++h2)
-#pragma unroll
-          for (int db = 0; db < DBLK; ++db) {
-            const int r0 = qb * 32 + h2 * 16;
-            dv[db] = mfma32x32x16(pf[h2], lo.tr_frag(Gd, r0, db), dv[db]);
-            dk[db] = mfma32x32x16(dsf[h2], lo.tr_frag(Q, r0, db), dk[db]);
-          }
+        // dV += P^T dO ; dK += dS^T Q (M = keys, N = d, K = the 32 queries of
+        // this half); step st = (h2 = st / DBLK, db = st % DBLK)
+        pipelined<2 * DBLK, 2>(
+            [&](int st) {
+              const int r0 = qb * 32 + (st / DBLK) * 16;
+              return Frag2{lo.tr_frag(Gd, r0, st % DBLK), lo.tr_frag(Q, r0, st % DBLK)};
+            },
+            [&](int st, const Frag2& f) {
+              const int h2 = st / DBLK, db = st % DBLK;
+              dv[db] = mfma32x32x16(pf[h2], f.a, dv[db]);
+              dk[db] = mfma32x32x16(dsf[h2], f.b, dk[db]);
+            });
       }
-
 #pragma unroll
       for (int i = 0; i < DBLK; ++i) {
         pin_agpr(dk[i]);
         pin_agpr(dv[i]);
       }
+
       if (!has_next) break;
-      store_q(buf ^ 1);
+      store_stats(buf ^ 1);
       buf ^= 1;
     }
   }
@@ -666,6 +732,20 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(BwdParams p) {
     }
   }
 }
+
+// Every (KSTEPS, DBLK) variant the launchers dispatch to, instantiated
+// explicitly: with lambdas in the kernel bodies the host pass otherwise
+// emits launch stubs for only some of the implicitly instantiated kernels.
+#define HARP_RA_INSTANTIATE(KS, DB)                             \
+  template __global__ void fwd_kernel<KS, DB>(FwdParams);       \
+  template __global__ void dq_kernel<KS, DB>(BwdParams);        \
+  template __global__ void dkdv_kernel<KS, DB>(BwdParams);
+HARP_RA_INSTANTIATE(2, 1)
+HARP_RA_INSTANTIATE(4, 2)
+HARP_RA_INSTANTIATE(5, 3)
+HARP_RA_INSTANTIATE(6, 3)
+HARP_RA_INSTANTIATE(8, 4)
+#undef HARP_RA_INSTANTIATE
 
 // ---------------------------------------------------------------------------
 // Host-side launchers
