@@ -6,11 +6,11 @@ S_local=8192, D=128 — config 4: B=1, H=24, D=128, T=8192 local queries, KV
 streamed as 8 chunks of 8192 (8 ring steps, 65536 keys), bf16 N(0,1) inputs
 from seed 3407, non-causal.
 
-One step = the hot path once: ring_attention_forward (V panel pack + fused
-forward kernel), ring_attention_delta (D = rowsum(dO*O)), and
-ring_attention_backward (K/Q/dO panel packs + dK/dV kernel + dQ kernel),
-called through torch.ops.ring_attention_ops with every input and output
-resident in HBM.  FLOP_total = 14*B*H*T*L*D (fwd 4, bwd 10; L = valid keys).
+One step = the hot path once: ring_attention_forward (fused forward kernel),
+ring_attention_delta (D = rowsum(dO*O)), and ring_attention_backward (dK/dV
+kernel + dQ kernel), called through torch.ops.ring_attention_ops with every
+input and output resident in HBM.  FLOP_total = 14*B*H*T*L*D (fwd 4, bwd 10;
+L = valid keys).
 
 Prints ONE JSON line.  --gpus N with N > 1 is refused: this build measures one
 GPU (multi-GPU sharding is a design, not a measured path).
@@ -27,6 +27,12 @@ import time
 
 PEAK_BF16_TFLOPS = 2516.6  # 256 CU x 2.4 GHz x 4096 FLOP/clk/CU (dense)
 PEAK_HBM_GBS = 8000.0
+
+# HBM bytes per launch (read + write) of each kernel at config 4, measured
+# with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE, each scaled by what the same
+# counter reads for a 1 GiB device copy in the same run (FETCH x2.0, WRITE
+# x1.0).  Source: profiles/ring_attn_config4_counters.md.
+MEASURED_TRAFFIC_BYTES = {4: {"fwd": 988.5e6, "dkdv": 3251.7e6, "dq": 958.9e6, "delta": 151.8e6}}
 
 CONFIGS = {
     1: dict(B=1, H=8, T=512, D=64, N=1, tc=512, lens=None, vscale=1.0),
@@ -83,40 +89,42 @@ def cpu_model() -> str:
 
 def cpu_baseline(cfg, target_s: float):
     """The reference algorithm as PyTorch CPU ops (oracle.cpu_baseline_fwd_bwd)
-    on a bounded sample of the workload: one head, a subset of query rows,
-    the full KV length.  Returns the cpu_baseline JSON object."""
+    on a bounded sample of the workload: query rows of one head (then whole
+    heads, one at a time) against the full KV length, sized from a short probe
+    to take about target_s.  Returns the cpu_baseline JSON object."""
     import torch
 
     from oracle import ring_attn_oracle as orc
 
     threads = cpu_threads()
     torch.set_num_threads(threads)
-    B, D, N, T, tc = 1, cfg["D"], cfg["N"], cfg["T"], cfg["tc"]
+    B, D, N, T, tc, H = 1, cfg["D"], cfg["N"], cfg["T"], cfg["tc"], cfg["H"]
     lens = cfg["lens"] or [tc] * N
     L = sum(lens)
     scale = 1.0 / math.sqrt(D)
 
-    def run(tq):
-        q, ks, vs, do = orc.make_inputs(B, 1, tq, D, N, seed=1, chunk_len=tc, value_scale=cfg["vscale"])
+    def run(tq, seed):
+        q, ks, vs, do = orc.make_inputs(B, 1, tq, D, N, seed=seed, chunk_len=tc, value_scale=cfg["vscale"])
         ks = [k[:, :, :n] for k, n in zip(ks, lens)]
         vs = [v[:, :, :n] for v, n in zip(vs, lens)]
         t0 = time.perf_counter()
         orc.cpu_baseline_fwd_bwd(q, ks, vs, do, scale)
         return time.perf_counter() - t0
 
-    run(64)  # warm up oneDNN / thread pool
-    tq = 128
-    dt = run(tq)
-    tq_target = int(min(T, max(128, tq * target_s / max(dt, 1e-3))) // 128 * 128)
-    tq = max(128, tq_target)
-    dt = run(tq)
-    flops = 14.0 * 1 * 1 * tq * L * D
+    run(64, 1)  # warm up oneDNN / thread pool
+    rows_target = 128 * target_s / max(run(128, 1), 1e-3)
+    if rows_target <= T:
+        tq, nh = max(128, int(rows_target) // 128 * 128), 1
+    else:
+        tq, nh = T, int(min(H, max(1, rows_target // T)))
+    dt = sum(run(tq, 1 + i) for i in range(nh))
+    flops = 14.0 * nh * tq * L * D
     return {
         "value": round(flops / dt / 1e12, 4),
         "unit": "TFLOP/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"1 of {cfg['H']} heads x {tq} of {T} query rows against all {L} keys "
+        "sample": (f"{nh} of {H} heads x {tq} of {T} query rows against all {L} keys "
                    f"({N} chunks), fwd+bwd, {dt:.1f} s on {cpu_model()}"),
     }
 
@@ -245,7 +253,7 @@ def main() -> int:
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(dom_tf / PEAK_BF16_TFLOPS, 4),
-            "traffic": None,
+            "traffic": MEASURED_TRAFFIC_BYTES.get(args.config, {}).get(dom),
         },
         "cpu_baseline": None,
         "gpu": torch.cuda.get_device_name(0),
