@@ -74,8 +74,15 @@ struct PadTile {
   }
 };
 
+// The base and size are wave-uniform by construction; readfirstlane tells the
+// compiler so, which keeps the descriptor in SGPRs (a descriptor it believes
+// divergent costs a waterfall loop around every load).
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+  const uint64_t a = (uint64_t)base;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  const int n = __builtin_amdgcn_readfirstlane((int)bytes);
+  return __builtin_amdgcn_make_buffer_rsrc((void*)(((uint64_t)hi << 32) | lo), (short)0, n, 0x00020000);
 }
 
 // Buffer resource over rows [row0, row0 + rows) of a [rows][stride] bf16 view.
@@ -553,22 +560,32 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(BwdParams p) {
 // Backward dK/dV (KV-stationary, as ring_attn.cpp:2723-2816)
 // ---------------------------------------------------------------------------
 // Block = 4 waves x 32 keys.  The block's 128 K and V rows are copied to LDS
-// once and each wave keeps its 32 rows as MFMA B operands in AGPRs; the loop
-// streams 64-query tiles of Q / dO (+ LSE, D) through double-buffered LDS and
-// handles each tile as two 32-query halves.  Pad keys (past the chunk's valid
-// length) are written as zero at the end instead of being masked per tile:
-// in this layout a key's P / dS only reach its own dK / dV rows.
+// once and each wave keeps its 32 rows as MFMA B operands in registers; the
+// loop streams 64-query tiles of Q / dO (+ per-query LSE and D) through
+// double-buffered LDS and handles each tile as two 32-query halves.  Per half:
+//   A: S = Q K^T, dP = dO V^T          (MFMA; C row = query, col = key)
+//   B: P = exp2(S c - LSE2), dS = P (dP - D)        (VALU)
+//   C: dV += P^T dO, dK += dS^T Q      (MFMA; dO^T / Q^T read transposed)
+// One wave per SIMD, so the VALU work of B is hidden by interleaving it, a
+// pair of elements at a time, between the MFMAs of a neighbouring phase:
+//   tile t:  A(t,0)  ->  A(t,1) | B(t,0)  ->  C(t,0) | B(t,1)  ->  C(t,1)  ->  barrier
+// The barrier publishes tile t+1 and frees tile t's buffer for tile t+2's
+// loads, which then complete under a whole tile of MFMA work.
+// Pad keys (past the chunk's valid length) are written as zero at the end
+// instead of being masked per tile: a key's P / dS only reach its own dK / dV.
 template <int KSTEPS, int DBLK>
 __global__ __launch_bounds__(256, 1) void dkdv_kernel(BwdParams p) {
   constexpr int DP = DBLK * 32;
   using GK = PadTile<DP>;  // the block's K / V rows: row fragments only
   using GQ = XorTile<DP>;  // Q / dO tiles: row and transposed fragments
+  constexpr int NPAIR = 8;                                   // element pairs of B per half
+  constexpr int PA = (NPAIR + KSTEPS - 1) / KSTEPS;          // pairs per A step
+  constexpr int PC = (NPAIR + 2 * DBLK - 1) / (2 * DBLK);    // pairs per C step
   __shared__ __attribute__((aligned(16))) bf16 Kb[2 * GK::ELEMS];  // 128 key rows
   __shared__ __attribute__((aligned(16))) bf16 Vb[2 * GK::ELEMS];
   __shared__ __attribute__((aligned(16))) bf16 Qs[2][GQ::ELEMS];
   __shared__ __attribute__((aligned(16))) bf16 Gs[2][GQ::ELEMS];
-  __shared__ __attribute__((aligned(16))) float Ls[2][64];
-  __shared__ __attribute__((aligned(16))) float Dls[2][64];
+  __shared__ __attribute__((aligned(16))) float St[2][128];  // per query: (LSE2, D)
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, g = lane >> 5;
@@ -595,6 +612,41 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(BwdParams p) {
   if (kblk0 < len) {  // block has at least one valid key (block-uniform)
     XorLanes<DP, KSTEPS> lo;
     lo.init(lane);
+    DirectLoader<GQ, 4> qld, gld;
+    qld.init(p.sqt, p.D, wave, lane);
+    gld.init(p.sdt, p.D, wave, lane);
+    const bf16* qb_ = p.q + (int64_t)b * p.sqb + (int64_t)h * p.sqh;
+    const bf16* gb_ = p.dout + (int64_t)b * p.sdb + (int64_t)h * p.sdh;
+    const int64_t sbase = ((int64_t)b * p.H + h) * p.T;
+
+    // Per-query statistics of the next tile: wave 0 loads the raw m / l / D
+    // bits when it issues the tile and converts them only in store_stats,
+    // after the wait that precedes the barrier, so no wave ever stalls on
+    // these loads' latency.
+    uint32_t m_bits = 0, l_bits = 0, d_bits = 0;
+    auto issue = [&](int q0, int bf) {
+      qld.load(rows_rsrc(qb_, p.sqt, q0, p.T - q0), Qs[bf]);
+      gld.load(rows_rsrc(gb_, p.sdt, q0, p.T - q0), Gs[bf]);
+      if (tid < 64) {
+        const int qq = q0 + tid;
+        m_bits = l_bits = d_bits = 0;  // l = 0 marks a row past T: P = 0
+        if (qq < p.T) {
+          const int64_t i = sbase + qq;
+          m_bits = p.m_bf16 ? (uint32_t)((const uint16_t*)p.m)[i] : ((const uint32_t*)p.m)[i];
+          l_bits = ((const uint32_t*)p.l)[i];
+          d_bits = ((const uint32_t*)p.delta)[i];
+        }
+      }
+    };
+    auto store_stats = [&](int bf) {
+      if (tid < 64) {
+        const float mm = __uint_as_float(p.m_bf16 ? m_bits << 16 : m_bits);
+        const float ll = __uint_as_float(l_bits);
+        const float lse2 = (ll > 0.f) ? (mm + __logf(ll)) * kLog2e : INFINITY;
+        *(float2*)&St[bf][2 * tid] = make_float2(lse2, __uint_as_float(d_bits));
+      }
+    };
+
     bf16x8 kf[KSTEPS], vf[KSTEPS];
     {
       DirectLoader<GK, 4> kvl;
@@ -606,104 +658,151 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(BwdParams p) {
         kvl.load(rows_rsrc(p.ct.k[c] + kvo, p.skt, r0, len - r0), Kb + half * GK::ELEMS);
         kvl.load(rows_rsrc(p.ct.v[c] + kvo, p.skt, r0, len - r0), Vb + half * GK::ELEMS);
       }
+      issue(0, 0);
       wait_lds_loads();
+      store_stats(0);
       __syncthreads();
-      // this wave's 32 K / V rows as MFMA B operands, held in AGPRs for the
-      // whole loop (MFMA reads B from AGPRs directly)
+      // this wave's 32 K / V rows as MFMA B operands for the whole loop
       PadRows<DP> klo;
       klo.init(lane);
 #pragma unroll
       for (int ks = 0; ks < KSTEPS; ++ks) {
         kf[ks] = klo.frag(Kb, wave, ks);
         vf[ks] = klo.frag(Vb, wave, ks);
-        pin_agpr(kf[ks]);
-        pin_agpr(vf[ks]);
       }
     }
-    DirectLoader<GQ, 4> qld, gld;
-    qld.init(p.sqt, p.D, wave, lane);
-    gld.init(p.sdt, p.D, wave, lane);
-    const bf16* qb_ = p.q + (int64_t)b * p.sqb + (int64_t)h * p.sqh;
-    const bf16* gb_ = p.dout + (int64_t)b * p.sdb + (int64_t)h * p.sdh;
-    const int64_t sbase = ((int64_t)b * p.H + h) * p.T;
+    const int n_tiles = (p.T + 63) >> 6;
+    if (n_tiles > 1) issue(64, 1);
 
-    float lse_r = INFINITY, dl_r = 0.f;
-    auto issue = [&](int q0, int bf) {
-      qld.load(rows_rsrc(qb_, p.sqt, q0, p.T - q0), Qs[bf]);
-      gld.load(rows_rsrc(gb_, p.sdt, q0, p.T - q0), Gs[bf]);
-      if (tid < 64) {
-        const int qq = q0 + tid;
-        lse_r = (qq < p.T) ? lse2_of(p.m, p.m_bf16, p.l, sbase + qq) : INFINITY;
-        dl_r = (qq < p.T) ? p.delta[sbase + qq] : 0.f;
-      }
+    // (LSE2, D) of the rows of element pair j (C rows 2j, 2j+1 of this lane:
+    // consecutive queries) of half qb
+    auto stats_pair = [&](int bf, int qb, int j) {
+      return *(const f32x4*)&St[bf][2 * (qb * 32 + c_row(2 * j, g))];
     };
-    auto store_stats = [&](int bf) {
-      if (tid < 64) {
-        Ls[bf][tid] = lse_r;
-        Dls[bf][tid] = dl_r;
-      }
+    // B for element pair j of one half
+    auto pds_pair = [&](const f32x16& s, const f32x16& dp, int j, const f32x4& st, bf16x8* pf, bf16x8* dsf) {
+      const int r = 2 * j;
+      const float p0 = fast_exp2(__builtin_fmaf(s[r], c2, -st[0]));
+      const float p1 = fast_exp2(__builtin_fmaf(s[r + 1], c2, -st[2]));
+      pf[r >> 3][r & 7] = (bf16)p0;
+      pf[r >> 3][(r & 7) + 1] = (bf16)p1;
+      dsf[r >> 3][r & 7] = (bf16)(p0 * (dp[r] - st[1]));
+      dsf[r >> 3][(r & 7) + 1] = (bf16)(p1 * (dp[r + 1] - st[3]));
     };
-    issue(0, 0);
-    store_stats(0);
+    // A without interleaved VALU work
+    auto phase_a = [&](const bf16* Q, const bf16* Gd, int qb, f32x16& s, f32x16& dp) {
+      s = zero16();
+      dp = zero16();
+      pipelined<KSTEPS, 2>([&](int ks) { return Frag2{lo.row_frag(Q, qb, ks), lo.row_frag(Gd, qb, ks)}; },
+                           [&](int ks, const Frag2& f) {
+                             s = mfma32x32x16(f.a, kf[ks], s);
+                             dp = mfma32x32x16(f.b, vf[ks], dp);
+                           });
+    };
+    // C without interleaved VALU work; step st = (h2 = st / DBLK, db = st % DBLK)
+    auto phase_c = [&](const bf16* Q, const bf16* Gd, int qb, const bf16x8* pf, const bf16x8* dsf) {
+      pipelined<2 * DBLK, 2>(
+          [&](int st) {
+            const int r0 = qb * 32 + (st / DBLK) * 16;
+            return Frag2{lo.tr_frag(Gd, r0, st % DBLK), lo.tr_frag(Q, r0, st % DBLK)};
+          },
+          [&](int st, const Frag2& f) {
+            const int h2 = st / DBLK, db = st % DBLK;
+            dv[db] = mfma32x32x16(pf[h2], f.a, dv[db]);
+            dk[db] = mfma32x32x16(dsf[h2], f.b, dk[db]);
+          });
+    };
+    struct FragA {
+      bf16x8 a, b;
+      f32x4 st[PA];
+    };
+    struct FragC {
+      bf16x8 a, b;
+      f32x4 st[PC];
+    };
+
     int buf = 0;
 #pragma unroll 1
-    for (int q0 = 0; q0 < p.T; q0 += 64) {
-      const bool has_next = q0 + 64 < p.T;
-      wait_lds_loads();
-      __syncthreads();
-      if (has_next) issue(q0 + 64, buf ^ 1);
+    for (int t = 0;; ++t) {
       const bf16* Q = Qs[buf];
       const bf16* Gd = Gs[buf];
-
 #pragma unroll
       for (int i = 0; i < DBLK; ++i) {
         pin_agpr(dk[i]);
         pin_agpr(dv[i]);
       }
-      // per 32-query half: S = Q K^T, dP = dO V^T (C row = query, col = key),
-      // then P, dS and the dV / dK updates of that half
+      f32x16 s0, dp0, s1, dp1;
+      bf16x8 pf0[2], dsf0[2], pf1[2], dsf1[2];
+      // A(t,0)
+      phase_a(Q, Gd, 0, s0, dp0);
+
+      // A(t,1) | B(t,0)
+      s1 = zero16();
+      dp1 = zero16();
+      pipelined<KSTEPS, 2>(
+          [&](int ks) {
+            FragA f;
+            f.a = lo.row_frag(Q, 1, ks);
+            f.b = lo.row_frag(Gd, 1, ks);
+            const int j0 = ks * NPAIR / KSTEPS, j1 = (ks + 1) * NPAIR / KSTEPS;
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
-        f32x16 s = zero16(), dp = zero16();
-        pipelined<KSTEPS, 2>([&](int ks) { return Frag2{lo.row_frag(Q, qb, ks), lo.row_frag(Gd, qb, ks)}; },
-                             [&](int ks, const Frag2& f) {
-                               s = mfma32x32x16(f.a, kf[ks], s);
-                               dp = mfma32x32x16(f.b, vf[ks], dp);
-                             });
-        bf16x8 pf[2], dsf[2];
+            for (int u = 0; u < PA; ++u)
+              if (j0 + u < j1) f.st[u] = stats_pair(buf, 0, j0 + u);
+            return f;
+          },
+          [&](int ks, const FragA& f) {
+            const int j0 = ks * NPAIR / KSTEPS, j1 = (ks + 1) * NPAIR / KSTEPS, jm = (j0 + j1 + 1) / 2;
+            s1 = mfma32x32x16(f.a, kf[ks], s1);
+            sched_fence();
 #pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) {
-          const f32x4 lse4 = *(const f32x4*)(&Ls[buf][qb * 32 + 8 * i4 + 4 * g]);
-          const f32x4 dl4 = *(const f32x4*)(&Dls[buf][qb * 32 + 8 * i4 + 4 * g]);
+            for (int j = j0; j < jm; ++j) pds_pair(s0, dp0, j, f.st[j - j0], pf0, dsf0);
+            sched_fence();
+            dp1 = mfma32x32x16(f.b, vf[ks], dp1);
+            sched_fence();
 #pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const int r = i4 * 4 + t;
-            const float pv = fast_exp2(__builtin_fmaf(s[r], c2, -lse4[t]));
-            pf[r >> 3][r & 7] = (bf16)pv;
-            dsf[r >> 3][r & 7] = (bf16)(pv * (dp[r] - dl4[t]));
-          }
-        }
-        // dV += P^T dO ; dK += dS^T Q (M = keys, N = d, K = the 32 queries of
-        // this half); step st = (h2 = st / DBLK, db = st % DBLK)
-        pipelined<2 * DBLK, 2>(
-            [&](int st) {
-              const int r0 = qb * 32 + (st / DBLK) * 16;
-              return Frag2{lo.tr_frag(Gd, r0, st % DBLK), lo.tr_frag(Q, r0, st % DBLK)};
-            },
-            [&](int st, const Frag2& f) {
-              const int h2 = st / DBLK, db = st % DBLK;
-              dv[db] = mfma32x32x16(pf[h2], f.a, dv[db]);
-              dk[db] = mfma32x32x16(dsf[h2], f.b, dk[db]);
-            });
-      }
+            for (int j = jm; j < j1; ++j) pds_pair(s0, dp0, j, f.st[j - j0], pf0, dsf0);
+          });
+
+      // C(t,0) | B(t,1)
+      pipelined<2 * DBLK, 2>(
+          [&](int st) {
+            FragC f;
+            const int r0 = (st / DBLK) * 16;
+            f.a = lo.tr_frag(Gd, r0, st % DBLK);
+            f.b = lo.tr_frag(Q, r0, st % DBLK);
+            const int j0 = st * NPAIR / (2 * DBLK), j1 = (st + 1) * NPAIR / (2 * DBLK);
+#pragma unroll
+            for (int u = 0; u < PC; ++u)
+              if (j0 + u < j1) f.st[u] = stats_pair(buf, 1, j0 + u);
+            return f;
+          },
+          [&](int st, const FragC& f) {
+            const int h2 = st / DBLK, db = st % DBLK;
+            const int j0 = st * NPAIR / (2 * DBLK), j1 = (st + 1) * NPAIR / (2 * DBLK), jm = (j0 + j1 + 1) / 2;
+            dv[db] = mfma32x32x16(pf0[h2], f.a, dv[db]);
+            sched_fence();
+#pragma unroll
+            for (int j = j0; j < jm; ++j) pds_pair(s1, dp1, j, f.st[j - j0], pf1, dsf1);
+            sched_fence();
+            dk[db] = mfma32x32x16(dsf0[h2], f.b, dk[db]);
+            sched_fence();
+#pragma unroll
+            for (int j = jm; j < j1; ++j) pds_pair(s1, dp1, j, f.st[j - j0], pf1, dsf1);
+          });
+
+      // C(t,1)
+      phase_c(Q, Gd, 1, pf1, dsf1);
 #pragma unroll
       for (int i = 0; i < DBLK; ++i) {
         pin_agpr(dk[i]);
         pin_agpr(dv[i]);
       }
 
-      if (!has_next) break;
+      if (t + 1 >= n_tiles) break;
+      wait_lds_loads();
       store_stats(buf ^ 1);
+      __syncthreads();  // tile t+1 published; every wave is done with tile t
+      if (t + 2 < n_tiles) issue((t + 2) * 64, buf);
       buf ^= 1;
     }
   }
