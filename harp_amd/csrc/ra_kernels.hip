@@ -29,7 +29,7 @@ namespace harp_ra {
 
 typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
 typedef __attribute__((address_space(3))) void lds_void;
-typedef __amdgpu_buffer_rsrc_t rsrc_t;
+typedef uint32_t rsrc_t __attribute__((ext_vector_type(4)));  // buffer resource (V#), SGPR quad
 
 constexpr uint32_t kOOB = 0x80000000u;  // buffer offset past every valid range: loads 0
 
@@ -74,21 +74,47 @@ struct PadTile {
   }
 };
 
-// The base and size are wave-uniform by construction; readfirstlane tells the
-// compiler so, which keeps the descriptor in SGPRs (a descriptor it believes
-// divergent costs a waterfall loop around every load).
+// Raw buffer descriptor: base address, stride 0, num_records = bytes, and the
+// dword-3 format word of an untyped buffer.  The base and size are
+// wave-uniform by construction; readfirstlane tells the compiler so, which
+// keeps the descriptor in SGPRs.
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   const uint64_t a = (uint64_t)base;
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
-  const int n = __builtin_amdgcn_readfirstlane((int)bytes);
-  return __builtin_amdgcn_make_buffer_rsrc((void*)(((uint64_t)hi << 32) | lo), (short)0, n, 0x00020000);
+  rsrc_t r;
+  r.x = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  r.y = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32)) & 0xffffu;
+  r.z = __builtin_amdgcn_readfirstlane(bytes);
+  r.w = 0x00020000u;
+  return r;
 }
 
 // Buffer resource over rows [row0, row0 + rows) of a [rows][stride] bf16 view.
 __device__ __forceinline__ rsrc_t rows_rsrc(const bf16* base, int64_t stride, int row0, int rows) {
   return make_rsrc(base + (int64_t)row0 * stride, (uint32_t)((int64_t)(rows > 0 ? rows : 0) * stride * 2));
 }
+
+// One direct-to-LDS copy: every lane's 16 bytes at buffer offset voff land at
+// LDS byte address lds + 16 * lane (M0 holds the wave-uniform base; one wait
+// state separates the M0 write from its use).
+// Issued as inline asm on purpose: the compiler cannot tell which LDS buffer
+// an LDS-DMA load writes, so for the builtin it makes every later LDS read
+// wait for the load (s_waitcnt vmcnt(0)), which turns the double-buffered
+// prefetch into a synchronous load per tile.  Completion is instead ordered
+// explicitly: wait_lds_loads() then a barrier, before any wave reads the
+// buffer, and no load targets a buffer until a barrier shows that every wave
+// has finished reading it.
+__device__ __forceinline__ void lds_dma_b128(rsrc_t rs, uint32_t lds, uint32_t voff) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %1, %2, 0 offen lds"
+      :
+      : "s"(lds), "v"(voff), "s"(rs)
+      : "memory", "m0");
+}
+
+// Wait for this thread's direct-to-LDS loads (a barrier then publishes them).
+__device__ __forceinline__ void wait_lds_loads() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // This wave's share of the direct-to-LDS copies of one 64-row tile: slot
 // instruction i (64 slots) goes to waves round-robin; voff holds each lane's
@@ -115,14 +141,60 @@ struct DirectLoader {
 #pragma unroll
     for (int k = 0; k < kInst; ++k) {
       const int inst = wave + k * NW;
-      if (kInstTot % NW == 0 || inst < kInstTot)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(tile + inst * 512), 16, voff[k], 0, 0, 0);
+      if (kInstTot % NW == 0 || inst < kInstTot) {
+        const uint32_t lds = (uint32_t)(uintptr_t)(lds_void*)(tile + inst * 512);
+        lds_dma_b128(rs, __builtin_amdgcn_readfirstlane(lds), voff[k]);
+      }
     }
   }
 };
 
-// Wait for this thread's direct-to-LDS loads (a barrier then publishes them).
-__device__ __forceinline__ void wait_lds_loads() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Register-staged copy of one 64-row tile, same slot mapping as
+// DirectLoader: fetch() brings each lane's 16-byte slots global -> VGPRs
+// (compiler-visible buffer loads, range-checked like the direct copies);
+// store() writes them with one ds_write_b128 per slot.  Costs registers for
+// the staged slots but writes LDS at full ds_write rate, where a direct copy
+// ties the LDS up for much longer per byte.
+template <class G, int NW>
+struct StagedLoader {
+  static constexpr int kInstTot = G::SLOTS / 64;
+  static constexpr int kInst = (kInstTot + NW - 1) / NW;
+  uint32_t voff[kInst];
+  bf16x8 data[kInst];
+  int wave, lane;
+  __device__ __forceinline__ void init(int64_t row_stride, int D, int wave_, int lane_) {
+    wave = wave_;
+    lane = lane_;
+#pragma unroll
+    for (int k = 0; k < kInst; ++k) {
+      const int inst = wave + k * NW;
+      int r, c;
+      G::slot(inst * 64 + lane, r, c);
+      const bool ok = inst < kInstTot && c < G::NCH && c * 8 < D;
+      voff[k] = ok ? (uint32_t)(r * row_stride * 2 + c * 16) : kOOB;
+    }
+  }
+  __device__ __forceinline__ void fetch(const bf16* base, uint32_t bytes) {
+    const uint64_t a = (uint64_t)base;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(((uint64_t)hi << 32) | lo), (short)0, (int)__builtin_amdgcn_readfirstlane(bytes), 0x00020000);
+#pragma unroll
+    for (int k = 0; k < kInst; ++k) {
+      const int inst = wave + k * NW;
+      if (kInstTot % NW == 0 || inst < kInstTot)
+        data[k] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)voff[k], 0, 0));
+    }
+  }
+  __device__ __forceinline__ void store(bf16* tile) const {
+#pragma unroll
+    for (int k = 0; k < kInst; ++k) {
+      const int inst = wave + k * NW;
+      if (kInstTot % NW == 0 || inst < kInstTot) *(bf16x8*)(tile + (inst * 64 + lane) * 8) = data[k];
+    }
+  }
+};
 
 // Row fragment T[rb*32 + l32][16*ks + 8*g .. +7] of a PadTile: per-lane base,
 // immediate per (rb, ks).
@@ -186,6 +258,14 @@ struct XorLanes {
 // shuttles them between register files inside the loops nor crowds the VGPRs.
 __device__ __forceinline__ void pin_agpr(f32x16& x) { asm volatile("" : "+a"(x)); }
 __device__ __forceinline__ void pin_agpr(bf16x8& x) { asm volatile("" : "+a"(x)); }
+// Settle a value loaded from global memory before the main loop.  The
+// direct-to-LDS loads are invisible to the compiler, but they count in the
+// same hardware vmcnt: a wait the compiler places inside the loop for a
+// prologue load would also wait for the tile loads just issued.  An asm that
+// reads (and nominally rewrites) the value makes the compiler wait once,
+// here, and leaves nothing for it to wait on inside the loop.
+__device__ __forceinline__ void settle(bf16x8& x) { asm volatile("" : "+v"(x)); }
+__device__ __forceinline__ void settle(float& x) { asm volatile("" : "+v"(x)); }
 
 // Scheduling fence: the compiler may not move any instruction across it.
 __device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
@@ -260,7 +340,8 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(FwdParams p) {
   __shared__ __attribute__((aligned(16))) bf16 Ks[2][GK::ELEMS];
   __shared__ __attribute__((aligned(16))) bf16 Vs[2][GV::ELEMS];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // the wave index is wave-uniform; readfirstlane lets the compiler keep it in an SGPR
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, g = lane >> 5;
   int qt, h, b;
   decode_block((p.T + 127) / 128, p.H, qt, h, b);
@@ -304,6 +385,8 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(FwdParams p) {
   while (step < p.ct.n && p.ct.len[p.ct.order[step]] == 0) ++step;
   int buf = 0;
   if (step < p.ct.n) issue(step, 0, 0);
+#pragma unroll
+  for (int ks = 0; ks < KSTEPS; ++ks) settle(qf[ks]);
 #pragma unroll 1
   while (step < p.ct.n) {
     const int kv_left = p.ct.len[p.ct.order[step]] - k0;
@@ -451,7 +534,8 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(BwdParams p) {
   __shared__ __attribute__((aligned(16))) bf16 Ks[2][GK::ELEMS];
   __shared__ __attribute__((aligned(16))) bf16 Vs[2][GV::ELEMS];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // the wave index is wave-uniform; readfirstlane lets the compiler keep it in an SGPR
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, g = lane >> 5;
   int qt, h, b;
   decode_block((p.T + 127) / 128, p.H, qt, h, b);
@@ -498,6 +582,14 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(BwdParams p) {
   while (step < p.ct.n && p.ct.len[p.ct.order[step]] == 0) ++step;
   int buf = 0;
   if (step < p.ct.n) issue(step, 0, 0);
+#pragma unroll
+  for (int ks = 0; ks < KSTEPS; ++ks) {
+    settle(qf[ks]);
+    settle(gf[ks]);
+  }
+  float lse2_s = lse2, dlt_s = dlt;
+  settle(lse2_s);
+  settle(dlt_s);
 #pragma unroll 1
   while (step < p.ct.n) {
     int nstep, nk0;
@@ -526,8 +618,8 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(BwdParams p) {
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float pv = fast_exp2(__builtin_fmaf(s[kb][r], c2, -lse2));
-        dsf[kb * 2 + (r >> 3)][r & 7] = (bf16)(pv * (dp[kb][r] - dlt));
+        const float pv = fast_exp2(__builtin_fmaf(s[kb][r], c2, -lse2_s));
+        dsf[kb * 2 + (r >> 3)][r & 7] = (bf16)(pv * (dp[kb][r] - dlt_s));
       }
 
     // dQ^T += K^T dS^T; step i = (ks2 = i / DBLK, db = i % DBLK)
@@ -587,7 +679,8 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(BwdParams p) {
   __shared__ __attribute__((aligned(16))) bf16 Gs[2][GQ::ELEMS];
   __shared__ __attribute__((aligned(16))) float St[2][128];  // per query: (LSE2, D)
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // the wave index is wave-uniform; readfirstlane lets the compiler keep it in an SGPR
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, g = lane >> 5;
   int kt, h, b;
   decode_block(p.n_key_tiles, p.H, kt, h, b);
@@ -612,21 +705,23 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(BwdParams p) {
   if (kblk0 < len) {  // block has at least one valid key (block-uniform)
     XorLanes<DP, KSTEPS> lo;
     lo.init(lane);
-    DirectLoader<GQ, 4> qld, gld;
+    StagedLoader<GQ, 4> qld, gld;
     qld.init(p.sqt, p.D, wave, lane);
     gld.init(p.sdt, p.D, wave, lane);
     const bf16* qb_ = p.q + (int64_t)b * p.sqb + (int64_t)h * p.sqh;
     const bf16* gb_ = p.dout + (int64_t)b * p.sdb + (int64_t)h * p.sdh;
     const int64_t sbase = ((int64_t)b * p.H + h) * p.T;
 
-    // Per-query statistics of the next tile: wave 0 loads the raw m / l / D
-    // bits when it issues the tile and converts them only in store_stats,
-    // after the wait that precedes the barrier, so no wave ever stalls on
-    // these loads' latency.
+    // Q / dO tiles are fetched into registers one iteration ahead and written
+    // to LDS at the end of the iteration, just before the barrier that
+    // publishes them.  Per-query statistics ride along: wave 0 loads the raw
+    // m / l / D bits with the tile and converts them only in store_tile, so no
+    // wave stalls on these loads' latency.
     uint32_t m_bits = 0, l_bits = 0, d_bits = 0;
-    auto issue = [&](int q0, int bf) {
-      qld.load(rows_rsrc(qb_, p.sqt, q0, p.T - q0), Qs[bf]);
-      gld.load(rows_rsrc(gb_, p.sdt, q0, p.T - q0), Gs[bf]);
+    // fetch tile q0 into registers (Q / dO slots, raw statistics)
+    auto issue = [&](int q0) {
+      qld.fetch(qb_ + (int64_t)q0 * p.sqt, (uint32_t)((int64_t)(p.T - q0) * p.sqt * 2));
+      gld.fetch(gb_ + (int64_t)q0 * p.sdt, (uint32_t)((int64_t)(p.T - q0) * p.sdt * 2));
       if (tid < 64) {
         const int qq = q0 + tid;
         m_bits = l_bits = d_bits = 0;  // l = 0 marks a row past T: P = 0
@@ -638,7 +733,10 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(BwdParams p) {
         }
       }
     };
-    auto store_stats = [&](int bf) {
+    // write the fetched tile into LDS buffer bf
+    auto store_tile = [&](int bf) {
+      qld.store(Qs[bf]);
+      gld.store(Gs[bf]);
       if (tid < 64) {
         const float mm = __uint_as_float(p.m_bf16 ? m_bits << 16 : m_bits);
         const float ll = __uint_as_float(l_bits);
@@ -658,9 +756,9 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(BwdParams p) {
         kvl.load(rows_rsrc(p.ct.k[c] + kvo, p.skt, r0, len - r0), Kb + half * GK::ELEMS);
         kvl.load(rows_rsrc(p.ct.v[c] + kvo, p.skt, r0, len - r0), Vb + half * GK::ELEMS);
       }
-      issue(0, 0);
+      issue(0);
+      store_tile(0);
       wait_lds_loads();
-      store_stats(0);
       __syncthreads();
       // this wave's 32 K / V rows as MFMA B operands for the whole loop
       PadRows<DP> klo;
@@ -672,7 +770,7 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(BwdParams p) {
       }
     }
     const int n_tiles = (p.T + 63) >> 6;
-    if (n_tiles > 1) issue(64, 1);
+    if (n_tiles > 1) issue(64);
 
     // (LSE2, D) of the rows of element pair j (C rows 2j, 2j+1 of this lane:
     // consecutive queries) of half qb
@@ -799,10 +897,9 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(BwdParams p) {
       }
 
       if (t + 1 >= n_tiles) break;
-      wait_lds_loads();
-      store_stats(buf ^ 1);
+      store_tile(buf ^ 1);
       __syncthreads();  // tile t+1 published; every wave is done with tile t
-      if (t + 2 < n_tiles) issue((t + 2) * 64, buf);
+      if (t + 2 < n_tiles) issue((t + 2) * 64);
       buf ^= 1;
     }
   }
