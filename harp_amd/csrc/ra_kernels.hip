@@ -270,28 +270,77 @@ __device__ __forceinline__ void settle(float& x) { asm volatile("" : "+v"(x)); }
 // Scheduling fence: the compiler may not move any instruction across it.
 __device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
 
+// Compile-time step index: converts to int, and generic lambdas can read it
+// as a constant expression (decltype(i)::value).
+template <int I>
+struct Int {
+  static constexpr int value = I;
+  constexpr operator int() const { return I; }
+};
+
 // N MFMA steps whose LDS operand fragments are issued PF steps ahead:
 // load(i) returns step i's fragments, mma(i, frags) issues its MFMAs.  The
 // fences keep each step's reads above the MFMAs of the earlier steps, so the
-// s_waitcnt before an MFMA leaves the later reads in flight.
+// s_waitcnt before an MFMA leaves the later reads in flight.  The steps are
+// expanded by template recursion, so every step index is a compile-time
+// constant however long the pipeline is.
+template <int I, int N, int PF, class Load, class Mma, class F>
+__device__ __forceinline__ void pipeline_steps(const Load& load, const Mma& mma, F* f) {
+  if constexpr (I < N) {
+    if constexpr (I + PF < N) f[(I + PF) % (PF + 1)] = load(Int<I + PF>{});
+    sched_fence();
+    mma(Int<I>{}, f[I % (PF + 1)]);
+    sched_fence();
+    pipeline_steps<I + 1, N, PF>(load, mma, f);
+  }
+}
+template <int I, int N, class Load, class F>
+__device__ __forceinline__ void pipeline_fill(const Load& load, F* f) {
+  if constexpr (I < N) {
+    f[I] = load(Int<I>{});
+    pipeline_fill<I + 1, N>(load, f);
+  }
+}
 template <int N, int PF, class Load, class Mma>
 __device__ __forceinline__ void pipelined(const Load& load, const Mma& mma) {
-  using F = decltype(load(0));
+  using F = decltype(load(Int<0>{}));
   F f[PF + 1];
-#pragma unroll
-  for (int i = 0; i < PF && i < N; ++i) f[i] = load(i);
-#pragma unroll
-  for (int i = 0; i < N; ++i) {
-    if (i + PF < N) f[(i + PF) % (PF + 1)] = load(i + PF);
-    sched_fence();
-    mma(i, f[i % (PF + 1)]);
-    sched_fence();
-  }
+  pipeline_fill<0, (PF < N ? PF : N)>(load, f);
+  pipeline_steps<0, N, PF>(load, mma, f);
 }
 
 struct Frag2 {
   bf16x8 a, b;
 };
+
+// DPP row_newbcast:R -- every lane of each 16-lane row receives lane R of
+// that row.  With x[l] = v(l % 16, l / 32) (rows 0,1 equal; rows 2,3 equal),
+// lane l receives v(R, l / 32): a per-register value that depends only on
+// the lane's half of the wave, without LDS traffic.
+template <int R>
+__device__ __forceinline__ float row_bcast(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x150 + R, 0xf, 0xf, true));
+}
+__device__ __forceinline__ float row_bcast(float x, int r) {  // r must fold to a constant
+  switch (r) {
+    case 0: return row_bcast<0>(x);
+    case 1: return row_bcast<1>(x);
+    case 2: return row_bcast<2>(x);
+    case 3: return row_bcast<3>(x);
+    case 4: return row_bcast<4>(x);
+    case 5: return row_bcast<5>(x);
+    case 6: return row_bcast<6>(x);
+    case 7: return row_bcast<7>(x);
+    case 8: return row_bcast<8>(x);
+    case 9: return row_bcast<9>(x);
+    case 10: return row_bcast<10>(x);
+    case 11: return row_bcast<11>(x);
+    case 12: return row_bcast<12>(x);
+    case 13: return row_bcast<13>(x);
+    case 14: return row_bcast<14>(x);
+    default: return row_bcast<15>(x);
+  }
+}
 
 __device__ __forceinline__ float wave_half_max(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -670,9 +719,7 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(BwdParams p) {
   constexpr int DP = DBLK * 32;
   using GK = PadTile<DP>;  // the block's K / V rows: row fragments only
   using GQ = XorTile<DP>;  // Q / dO tiles: row and transposed fragments
-  constexpr int NPAIR = 8;                                   // element pairs of B per half
-  constexpr int PA = (NPAIR + KSTEPS - 1) / KSTEPS;          // pairs per A step
-  constexpr int PC = (NPAIR + 2 * DBLK - 1) / (2 * DBLK);    // pairs per C step
+  constexpr int NPAIR = 8;  // element pairs of B per half (16 C registers)
   __shared__ __attribute__((aligned(16))) bf16 Kb[2 * GK::ELEMS];  // 128 key rows
   __shared__ __attribute__((aligned(16))) bf16 Vb[2 * GK::ELEMS];
   __shared__ __attribute__((aligned(16))) bf16 Qs[2][GQ::ELEMS];
@@ -772,53 +819,22 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(BwdParams p) {
     const int n_tiles = (p.T + 63) >> 6;
     if (n_tiles > 1) issue(64);
 
-    // (LSE2, D) of the rows of element pair j (C rows 2j, 2j+1 of this lane:
-    // consecutive queries) of half qb
-    auto stats_pair = [&](int bf, int qb, int j) {
-      return *(const f32x4*)&St[bf][2 * (qb * 32 + c_row(2 * j, g))];
+    // (LSE2, D) of query row c_row(lane % 16, g) of half qb: one read per lane
+    // per half; row_bcast then hands each C register r the values of its own
+    // row c_row(r, g).
+    auto stats_lane = [&](int bf, int qb) {
+      return *(const float2*)&St[bf][2 * (qb * 32 + c_row(lane & 15, g))];
     };
-    // B for element pair j of one half
-    auto pds_pair = [&](const f32x16& s, const f32x16& dp, int j, const f32x4& st, bf16x8* pf, bf16x8* dsf) {
+    // B for element pair j (C registers 2j, 2j+1) of one half
+    auto pds_pair = [&](const f32x16& s, const f32x16& dp, int j, const float2& st, bf16x8* pf, bf16x8* dsf) {
       const int r = 2 * j;
-      const float p0 = fast_exp2(__builtin_fmaf(s[r], c2, -st[0]));
-      const float p1 = fast_exp2(__builtin_fmaf(s[r + 1], c2, -st[2]));
+      const float p0 = fast_exp2(__builtin_fmaf(s[r], c2, -row_bcast(st.x, r)));
+      const float p1 = fast_exp2(__builtin_fmaf(s[r + 1], c2, -row_bcast(st.x, r + 1)));
       pf[r >> 3][r & 7] = (bf16)p0;
       pf[r >> 3][(r & 7) + 1] = (bf16)p1;
-      dsf[r >> 3][r & 7] = (bf16)(p0 * (dp[r] - st[1]));
-      dsf[r >> 3][(r & 7) + 1] = (bf16)(p1 * (dp[r + 1] - st[3]));
+      dsf[r >> 3][r & 7] = (bf16)(p0 * (dp[r] - row_bcast(st.y, r)));
+      dsf[r >> 3][(r & 7) + 1] = (bf16)(p1 * (dp[r + 1] - row_bcast(st.y, r + 1)));
     };
-    // A without interleaved VALU work
-    auto phase_a = [&](const bf16* Q, const bf16* Gd, int qb, f32x16& s, f32x16& dp) {
-      s = zero16();
-      dp = zero16();
-      pipelined<KSTEPS, 2>([&](int ks) { return Frag2{lo.row_frag(Q, qb, ks), lo.row_frag(Gd, qb, ks)}; },
-                           [&](int ks, const Frag2& f) {
-                             s = mfma32x32x16(f.a, kf[ks], s);
-                             dp = mfma32x32x16(f.b, vf[ks], dp);
-                           });
-    };
-    // C without interleaved VALU work; step st = (h2 = st / DBLK, db = st % DBLK)
-    auto phase_c = [&](const bf16* Q, const bf16* Gd, int qb, const bf16x8* pf, const bf16x8* dsf) {
-      pipelined<2 * DBLK, 2>(
-          [&](int st) {
-            const int r0 = qb * 32 + (st / DBLK) * 16;
-            return Frag2{lo.tr_frag(Gd, r0, st % DBLK), lo.tr_frag(Q, r0, st % DBLK)};
-          },
-          [&](int st, const Frag2& f) {
-            const int h2 = st / DBLK, db = st % DBLK;
-            dv[db] = mfma32x32x16(pf[h2], f.a, dv[db]);
-            dk[db] = mfma32x32x16(dsf[h2], f.b, dk[db]);
-          });
-    };
-    struct FragA {
-      bf16x8 a, b;
-      f32x4 st[PA];
-    };
-    struct FragC {
-      bf16x8 a, b;
-      f32x4 st[PC];
-    };
-
     int buf = 0;
 #pragma unroll 1
     for (int t = 0;; ++t) {
@@ -829,67 +845,62 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(BwdParams p) {
         pin_agpr(dk[i]);
         pin_agpr(dv[i]);
       }
-      f32x16 s0, dp0, s1, dp1;
+      f32x16 s0 = zero16(), dp0 = zero16(), s1 = zero16(), dp1 = zero16();
       bf16x8 pf0[2], dsf0[2], pf1[2], dsf1[2];
-      // A(t,0)
-      phase_a(Q, Gd, 0, s0, dp0);
-
-      // A(t,1) | B(t,0)
-      s1 = zero16();
-      dp1 = zero16();
-      pipelined<KSTEPS, 2>(
-          [&](int ks) {
-            FragA f;
-            f.a = lo.row_frag(Q, 1, ks);
-            f.b = lo.row_frag(Gd, 1, ks);
-            const int j0 = ks * NPAIR / KSTEPS, j1 = (ks + 1) * NPAIR / KSTEPS;
-#pragma unroll
-            for (int u = 0; u < PA; ++u)
-              if (j0 + u < j1) f.st[u] = stats_pair(buf, 0, j0 + u);
-            return f;
+      const float2 st0 = stats_lane(buf, 0), st1 = stats_lane(buf, 1);
+      // The tile's four phases run as one software pipeline of
+      // 2*KSTEPS + 4*DBLK steps (two MFMAs each), so the fragments of a
+      // phase's first steps are in flight while the previous phase finishes:
+      //   [0, SA)              A(t,0)
+      //   [SA, 2SA)            A(t,1) | B(t,0)
+      //   [2SA, 2SA+SC)        C(t,0) | B(t,1)
+      //   [2SA+SC, 2SA+2SC)    C(t,1)
+      constexpr int SA = KSTEPS, SC = 2 * DBLK;
+      pipelined<2 * SA + 2 * SC, 2>(
+          [&](auto ii) {
+            constexpr int i = decltype(ii)::value;
+            if constexpr (i < 2 * SA) {
+              return Frag2{lo.row_frag(Q, i / SA, i % SA), lo.row_frag(Gd, i / SA, i % SA)};
+            } else {
+              constexpr int c = i - 2 * SA, st = c % SC, r0 = (c / SC) * 32 + (st / DBLK) * 16;
+              return Frag2{lo.tr_frag(Gd, r0, st % DBLK), lo.tr_frag(Q, r0, st % DBLK)};
+            }
           },
-          [&](int ks, const FragA& f) {
-            const int j0 = ks * NPAIR / KSTEPS, j1 = (ks + 1) * NPAIR / KSTEPS, jm = (j0 + j1 + 1) / 2;
-            s1 = mfma32x32x16(f.a, kf[ks], s1);
-            sched_fence();
+          [&](auto ii, const Frag2& f) {
+            constexpr int i = decltype(ii)::value;
+            if constexpr (i < SA) {
+              s0 = mfma32x32x16(f.a, kf[i], s0);
+              dp0 = mfma32x32x16(f.b, vf[i], dp0);
+            } else if constexpr (i < 2 * SA) {
+              constexpr int ks = i - SA;
+              const int j0 = ks * NPAIR / SA, j1 = (ks + 1) * NPAIR / SA, jm = (j0 + j1 + 1) / 2;
+              s1 = mfma32x32x16(f.a, kf[ks], s1);
+              sched_fence();
 #pragma unroll
-            for (int j = j0; j < jm; ++j) pds_pair(s0, dp0, j, f.st[j - j0], pf0, dsf0);
-            sched_fence();
-            dp1 = mfma32x32x16(f.b, vf[ks], dp1);
-            sched_fence();
+              for (int j = j0; j < jm; ++j) pds_pair(s0, dp0, j, st0, pf0, dsf0);
+              sched_fence();
+              dp1 = mfma32x32x16(f.b, vf[ks], dp1);
+              sched_fence();
 #pragma unroll
-            for (int j = jm; j < j1; ++j) pds_pair(s0, dp0, j, f.st[j - j0], pf0, dsf0);
+              for (int j = jm; j < j1; ++j) pds_pair(s0, dp0, j, st0, pf0, dsf0);
+            } else if constexpr (i < 2 * SA + SC) {
+              constexpr int st = i - 2 * SA, h2 = st / DBLK, db = st % DBLK;
+              const int j0 = st * NPAIR / SC, j1 = (st + 1) * NPAIR / SC, jm = (j0 + j1 + 1) / 2;
+              dv[db] = mfma32x32x16(pf0[h2], f.a, dv[db]);
+              sched_fence();
+#pragma unroll
+              for (int j = j0; j < jm; ++j) pds_pair(s1, dp1, j, st1, pf1, dsf1);
+              sched_fence();
+              dk[db] = mfma32x32x16(dsf0[h2], f.b, dk[db]);
+              sched_fence();
+#pragma unroll
+              for (int j = jm; j < j1; ++j) pds_pair(s1, dp1, j, st1, pf1, dsf1);
+            } else {
+              constexpr int st = i - 2 * SA - SC, h2 = st / DBLK, db = st % DBLK;
+              dv[db] = mfma32x32x16(pf1[h2], f.a, dv[db]);
+              dk[db] = mfma32x32x16(dsf1[h2], f.b, dk[db]);
+            }
           });
-
-      // C(t,0) | B(t,1)
-      pipelined<2 * DBLK, 2>(
-          [&](int st) {
-            FragC f;
-            const int r0 = (st / DBLK) * 16;
-            f.a = lo.tr_frag(Gd, r0, st % DBLK);
-            f.b = lo.tr_frag(Q, r0, st % DBLK);
-            const int j0 = st * NPAIR / (2 * DBLK), j1 = (st + 1) * NPAIR / (2 * DBLK);
-#pragma unroll
-            for (int u = 0; u < PC; ++u)
-              if (j0 + u < j1) f.st[u] = stats_pair(buf, 1, j0 + u);
-            return f;
-          },
-          [&](int st, const FragC& f) {
-            const int h2 = st / DBLK, db = st % DBLK;
-            const int j0 = st * NPAIR / (2 * DBLK), j1 = (st + 1) * NPAIR / (2 * DBLK), jm = (j0 + j1 + 1) / 2;
-            dv[db] = mfma32x32x16(pf0[h2], f.a, dv[db]);
-            sched_fence();
-#pragma unroll
-            for (int j = j0; j < jm; ++j) pds_pair(s1, dp1, j, f.st[j - j0], pf1, dsf1);
-            sched_fence();
-            dk[db] = mfma32x32x16(dsf0[h2], f.b, dk[db]);
-            sched_fence();
-#pragma unroll
-            for (int j = jm; j < j1; ++j) pds_pair(s1, dp1, j, f.st[j - j0], pf1, dsf1);
-          });
-
-      // C(t,1)
-      phase_c(Q, Gd, 1, pf1, dsf1);
 #pragma unroll
       for (int i = 0; i < DBLK; ++i) {
         pin_agpr(dk[i]);
