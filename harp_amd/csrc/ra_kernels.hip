@@ -150,17 +150,19 @@ struct DirectLoader {
 };
 
 // Register-staged copy of one 64-row tile, same slot mapping as
-// DirectLoader: fetch() brings each lane's 16-byte slots global -> VGPRs
+// DirectLoader: fetch() brings each lane's 16-byte slots global -> registers
 // (compiler-visible buffer loads, range-checked like the direct copies);
-// store() writes them with one ds_write_b128 per slot.  Costs registers for
-// the staged slots but writes LDS at full ds_write rate, where a direct copy
-// ties the LDS up for much longer per byte.
+// store() writes them with one ds_write_b128 per slot.  The staged slots
+// live in a separate Data object, so several tiles can be in flight with
+// one set of offsets.
 template <class G, int NW>
 struct StagedLoader {
   static constexpr int kInstTot = G::SLOTS / 64;
   static constexpr int kInst = (kInstTot + NW - 1) / NW;
+  struct Data {
+    bf16x8 v[kInst];
+  };
   uint32_t voff[kInst];
-  bf16x8 data[kInst];
   int wave, lane;
   __device__ __forceinline__ void init(int64_t row_stride, int D, int wave_, int lane_) {
     wave = wave_;
@@ -174,25 +176,23 @@ struct StagedLoader {
       voff[k] = ok ? (uint32_t)(r * row_stride * 2 + c * 16) : kOOB;
     }
   }
-  __device__ __forceinline__ void fetch(const bf16* base, uint32_t bytes) {
+  __device__ __forceinline__ bool valid(int k) const { return kInstTot % NW == 0 || wave + k * NW < kInstTot; }
+  __device__ __forceinline__ void fetch(Data& d, const bf16* base, uint32_t bytes) const {
     const uint64_t a = (uint64_t)base;
     const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
     const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(((uint64_t)hi << 32) | lo), (short)0, (int)__builtin_amdgcn_readfirstlane(bytes), 0x00020000);
 #pragma unroll
-    for (int k = 0; k < kInst; ++k) {
-      const int inst = wave + k * NW;
-      if (kInstTot % NW == 0 || inst < kInstTot)
-        data[k] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)voff[k], 0, 0));
-    }
+    for (int k = 0; k < kInst; ++k)
+      if (valid(k)) d.v[k] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)voff[k], 0, 0));
   }
-  __device__ __forceinline__ void store(bf16* tile) const {
+  __device__ __forceinline__ void store_one(const Data& d, bf16* tile, int k) const {
+    if (valid(k)) *(bf16x8*)(tile + ((wave + k * NW) * 64 + lane) * 8) = d.v[k];
+  }
+  __device__ __forceinline__ void store(const Data& d, bf16* tile) const {
 #pragma unroll
-    for (int k = 0; k < kInst; ++k) {
-      const int inst = wave + k * NW;
-      if (kInstTot % NW == 0 || inst < kInstTot) *(bf16x8*)(tile + (inst * 64 + lane) * 8) = data[k];
-    }
+    for (int k = 0; k < kInst; ++k) store_one(d, tile, k);
   }
 };
 
@@ -759,36 +759,45 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(BwdParams p) {
     const bf16* gb_ = p.dout + (int64_t)b * p.sdb + (int64_t)h * p.sdh;
     const int64_t sbase = ((int64_t)b * p.H + h) * p.T;
 
-    // Q / dO tiles are fetched into registers one iteration ahead and written
-    // to LDS at the end of the iteration, just before the barrier that
+    // Q / dO tiles are fetched into registers two tiles ahead (two register
+    // sets alternate, so a fetch has two tiles of work to complete) and are
+    // written to the idle LDS buffer during the last MFMA phase of the tile
+    // before the one that reads them; the barrier that ends that tile
     // publishes them.  Per-query statistics ride along: wave 0 loads the raw
-    // m / l / D bits with the tile and converts them only in store_tile, so no
-    // wave stalls on these loads' latency.
-    uint32_t m_bits = 0, l_bits = 0, d_bits = 0;
-    // fetch tile q0 into registers (Q / dO slots, raw statistics)
-    auto issue = [&](int q0) {
-      qld.fetch(qb_ + (int64_t)q0 * p.sqt, (uint32_t)((int64_t)(p.T - q0) * p.sqt * 2));
-      gld.fetch(gb_ + (int64_t)q0 * p.sdt, (uint32_t)((int64_t)(p.T - q0) * p.sdt * 2));
+    // m / l / D bits with the tile and converts them only when it stores
+    // them, so no wave stalls on these loads' latency.
+    using QData = typename StagedLoader<GQ, 4>::Data;
+    QData qdat[2], gdat[2];
+    uint32_t m_bits[2] = {0, 0}, l_bits[2] = {0, 0}, d_bits[2] = {0, 0};
+    auto fetch_tile = [&](auto setc, int q0) {
+      constexpr int S = decltype(setc)::value;
+      qld.fetch(qdat[S], qb_ + (int64_t)q0 * p.sqt, (uint32_t)((int64_t)(p.T - q0) * p.sqt * 2));
+      gld.fetch(gdat[S], gb_ + (int64_t)q0 * p.sdt, (uint32_t)((int64_t)(p.T - q0) * p.sdt * 2));
       if (tid < 64) {
         const int qq = q0 + tid;
-        m_bits = l_bits = d_bits = 0;  // l = 0 marks a row past T: P = 0
+        m_bits[S] = l_bits[S] = d_bits[S] = 0;  // l = 0 marks a row past T: P = 0
         if (qq < p.T) {
           const int64_t i = sbase + qq;
-          m_bits = p.m_bf16 ? (uint32_t)((const uint16_t*)p.m)[i] : ((const uint32_t*)p.m)[i];
-          l_bits = ((const uint32_t*)p.l)[i];
-          d_bits = ((const uint32_t*)p.delta)[i];
+          m_bits[S] = p.m_bf16 ? (uint32_t)((const uint16_t*)p.m)[i] : ((const uint32_t*)p.m)[i];
+          l_bits[S] = ((const uint32_t*)p.l)[i];
+          d_bits[S] = ((const uint32_t*)p.delta)[i];
         }
       }
     };
-    // write the fetched tile into LDS buffer bf
-    auto store_tile = [&](int bf) {
-      qld.store(Qs[bf]);
-      gld.store(Gs[bf]);
+    constexpr int kQI = StagedLoader<GQ, 4>::kInst;
+    // slot j of set S (Q slots, then dO slots) into LDS buffer bf
+    auto store_slot = [&](auto setc, int bf, int j) {
+      constexpr int S = decltype(setc)::value;
+      if (j < kQI) qld.store_one(qdat[S], Qs[bf], j);
+      else gld.store_one(gdat[S], Gs[bf], j - kQI);
+    };
+    auto store_stats = [&](auto setc, int bf) {
+      constexpr int S = decltype(setc)::value;
       if (tid < 64) {
-        const float mm = __uint_as_float(p.m_bf16 ? m_bits << 16 : m_bits);
-        const float ll = __uint_as_float(l_bits);
+        const float mm = __uint_as_float(p.m_bf16 ? m_bits[S] << 16 : m_bits[S]);
+        const float ll = __uint_as_float(l_bits[S]);
         const float lse2 = (ll > 0.f) ? (mm + __logf(ll)) * kLog2e : INFINITY;
-        *(float2*)&St[bf][2 * tid] = make_float2(lse2, __uint_as_float(d_bits));
+        *(float2*)&St[bf][2 * tid] = make_float2(lse2, __uint_as_float(d_bits[S]));
       }
     };
 
@@ -803,8 +812,10 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(BwdParams p) {
         kvl.load(rows_rsrc(p.ct.k[c] + kvo, p.skt, r0, len - r0), Kb + half * GK::ELEMS);
         kvl.load(rows_rsrc(p.ct.v[c] + kvo, p.skt, r0, len - r0), Vb + half * GK::ELEMS);
       }
-      issue(0);
-      store_tile(0);
+      fetch_tile(Int<0>{}, 0);
+#pragma unroll
+      for (int j = 0; j < 2 * kQI; ++j) store_slot(Int<0>{}, 0, j);
+      store_stats(Int<0>{}, 0);
       wait_lds_loads();
       __syncthreads();
       // this wave's 32 K / V rows as MFMA B operands for the whole loop
@@ -817,7 +828,8 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(BwdParams p) {
       }
     }
     const int n_tiles = (p.T + 63) >> 6;
-    if (n_tiles > 1) issue(64);
+    if (n_tiles > 1) fetch_tile(Int<1>{}, 64);
+    if (n_tiles > 2) fetch_tile(Int<0>{}, 128);
 
     // (LSE2, D) of query row c_row(lane % 16, g) of half qb: one read per lane
     // per half; row_bcast then hands each C register r the values of its own
@@ -835,11 +847,13 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(BwdParams p) {
       dsf[r >> 3][r & 7] = (bf16)(p0 * (dp[r] - row_bcast(st.y, r)));
       dsf[r >> 3][(r & 7) + 1] = (bf16)(p1 * (dp[r + 1] - row_bcast(st.y, r + 1)));
     };
-    int buf = 0;
-#pragma unroll 1
-    for (int t = 0;; ++t) {
-      const bf16* Q = Qs[buf];
-      const bf16* Gd = Gs[buf];
+    // One 64-query tile t; S = t % 2 names its LDS buffer and the register
+    // set that holds tile t + 1 is 1 - S (compile-time, so the register sets
+    // are never indexed dynamically).  Returns true after the last tile.
+    auto tile = [&](auto setc, int t) -> bool {
+      constexpr int S = decltype(setc)::value;
+      const bf16* Q = Qs[S];
+      const bf16* Gd = Gs[S];
 #pragma unroll
       for (int i = 0; i < DBLK; ++i) {
         pin_agpr(dk[i]);
@@ -847,15 +861,17 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(BwdParams p) {
       }
       f32x16 s0 = zero16(), dp0 = zero16(), s1 = zero16(), dp1 = zero16();
       bf16x8 pf0[2], dsf0[2], pf1[2], dsf1[2];
-      const float2 st0 = stats_lane(buf, 0), st1 = stats_lane(buf, 1);
+      const float2 st0 = stats_lane(S, 0), st1 = stats_lane(S, 1);
       // The tile's four phases run as one software pipeline of
       // 2*KSTEPS + 4*DBLK steps (two MFMAs each), so the fragments of a
       // phase's first steps are in flight while the previous phase finishes:
       //   [0, SA)              A(t,0)
       //   [SA, 2SA)            A(t,1) | B(t,0)
       //   [2SA, 2SA+SC)        C(t,0) | B(t,1)
-      //   [2SA+SC, 2SA+2SC)    C(t,1)
-      constexpr int SA = KSTEPS, SC = 2 * DBLK;
+      //   [2SA+SC, 2SA+2SC)    C(t,1) | tile t+1 registers -> LDS buffer 1-S
+      // (buffer 1-S held tile t-1, which every wave finished before the
+      // barrier that ended tile t-1; past the last tile the stores are unused)
+      constexpr int SA = KSTEPS, SC = 2 * DBLK, NST = 2 * kQI;
       pipelined<2 * SA + 2 * SC, 2>(
           [&](auto ii) {
             constexpr int i = decltype(ii)::value;
@@ -898,6 +914,10 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(BwdParams p) {
             } else {
               constexpr int st = i - 2 * SA - SC, h2 = st / DBLK, db = st % DBLK;
               dv[db] = mfma32x32x16(pf1[h2], f.a, dv[db]);
+              sched_fence();
+#pragma unroll
+              for (int j = st * NST / SC; j < (st + 1) * NST / SC; ++j) store_slot(Int<1 - S>{}, 1 - S, j);
+              sched_fence();
               dk[db] = mfma32x32x16(dsf1[h2], f.b, dk[db]);
             }
           });
@@ -906,12 +926,16 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(BwdParams p) {
         pin_agpr(dk[i]);
         pin_agpr(dv[i]);
       }
-
-      if (t + 1 >= n_tiles) break;
-      store_tile(buf ^ 1);
+      if (t + 1 >= n_tiles) return true;
+      store_stats(Int<1 - S>{}, 1 - S);
       __syncthreads();  // tile t+1 published; every wave is done with tile t
-      if (t + 2 < n_tiles) issue((t + 2) * 64);
-      buf ^= 1;
+      if (t + 3 < n_tiles) fetch_tile(Int<1 - S>{}, (t + 3) * 64);
+      return false;
+    };
+#pragma unroll 1
+    for (int t = 0;; t += 2) {
+      if (tile(Int<0>{}, t)) break;
+      if (tile(Int<1>{}, t + 1)) break;
     }
   }
 
