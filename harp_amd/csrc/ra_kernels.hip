@@ -6,10 +6,10 @@
 // D = rowsum(dO * O) is the caller's preprocess (src/models/z_image/module/attn.py:41).
 //
 // Work split on one GPU (one rank's share, all ring steps in one launch each):
-//   fwd_kernel    per 128-query tile: S^T = K Q^T -> online softmax (lane = query)
+//   fwd_kernel    per 256-query tile: S^T = K Q^T -> online softmax (lane = query)
 //                 -> O^T += V^T P^T, over every 64-key tile of every chunk in ring order.
 //   delta_kernel  D = rowsum(dO * O) (fp32).
-//   dq_kernel     per 128-query tile: recompute S^T, dP^T, dS^T; dQ^T += K^T dS^T.
+//   dq_kernel     per 256-query tile: recompute S^T, dP^T, dS^T; dQ^T += K^T dS^T.
 //   dkdv_kernel   per 128-key tile (KV-stationary like the reference): per 64-query
 //                 tile recompute S, dP; dV += P^T dO, dK += dS^T Q.
 //
@@ -377,11 +377,16 @@ __device__ __forceinline__ void next_tile(const ChunkTable& ct, int step, int k0
 // ---------------------------------------------------------------------------
 // Forward
 // ---------------------------------------------------------------------------
+// Block = 8 waves x 32 queries (two waves per SIMD, one block per CU): every
+// K / V tile copied into LDS serves 256 queries, which halves the LDS-DMA
+// writes per MFMA against two 4-wave blocks per CU.
+constexpr int kFwdWaves = 8;
+constexpr int kFwdRows = 32 * kFwdWaves;
 // KSTEPS = ceil(D/16) k-steps of the S contraction; DBLK = ceil(D/32) row
-// blocks of O^T (DP = 32*DBLK >= 16*KSTEPS).  Block = 4 waves x 32 queries;
+// blocks of O^T (DP = 32*DBLK >= 16*KSTEPS).  Block = kFwdWaves waves x 32 queries;
 // 64-key tiles.
 template <int KSTEPS, int DBLK>
-__global__ __launch_bounds__(256, 2) void fwd_kernel(FwdParams p) {
+__global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
   constexpr int DP = DBLK * 32;
   using GK = PadTile<DP>;  // K: row fragments only
   using GV = XorTile<DP>;  // V: transposed fragments
@@ -393,8 +398,8 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(FwdParams p) {
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, g = lane >> 5;
   int qt, h, b;
-  decode_block((p.T + 127) / 128, p.H, qt, h, b);
-  const int qi = qt * 128 + wave * 32 + l32;
+  decode_block((p.T + kFwdRows - 1) / kFwdRows, p.H, qt, h, b);
+  const int qi = qt * kFwdRows + wave * 32 + l32;
   const bool q_ok = qi < p.T;
   const float c2 = p.scale * kLog2e;
 
@@ -411,9 +416,9 @@ __global__ __launch_bounds__(256, 2) void fwd_kernel(FwdParams p) {
   klo.init(lane);
   XorLanes<DP, KSTEPS> vlo;
   vlo.init(lane, false);
-  DirectLoader<GK, 4> kld;
+  DirectLoader<GK, kFwdWaves> kld;
   kld.init(p.skt, p.D, wave, lane);
-  DirectLoader<GV, 4> vld;
+  DirectLoader<GV, kFwdWaves> vld;
   vld.init(p.skt, p.D, wave, lane);
 
   f32x16 o[DBLK];
@@ -573,10 +578,14 @@ __device__ __forceinline__ float lse2_of(const void* m, int m_bf16, const float*
 // ---------------------------------------------------------------------------
 // Backward dQ (Q-stationary): dQ = scale * sum_c dS_c K_c
 // ---------------------------------------------------------------------------
+// Block = 8 waves x 32 queries (two waves per SIMD, one block per CU), for
+// the same reason as the forward: each K / V tile in LDS serves 256 queries.
+constexpr int kDqWaves = 8;
+constexpr int kDqRows = 32 * kDqWaves;
 // Pad keys need no mask here: their K/V rows load as zero, so their dS has
 // no effect on dQ^T = K^T dS^T.
 template <int KSTEPS, int DBLK>
-__global__ __launch_bounds__(256, 2) void dq_kernel(BwdParams p) {
+__global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
   constexpr int DP = DBLK * 32;
   using GK = XorTile<DP>;  // K: row and transposed fragments
   using GV = PadTile<DP>;  // V: row fragments only
@@ -587,8 +596,8 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(BwdParams p) {
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, g = lane >> 5;
   int qt, h, b;
-  decode_block((p.T + 127) / 128, p.H, qt, h, b);
-  const int qi = qt * 128 + wave * 32 + l32;
+  decode_block((p.T + kDqRows - 1) / kDqRows, p.H, qt, h, b);
+  const int qi = qt * kDqRows + wave * 32 + l32;
   const bool q_ok = qi < p.T;
   const float c2 = p.scale * kLog2e;
 
@@ -611,9 +620,9 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(BwdParams p) {
   klo.init(lane);
   PadRows<DP> vlo;
   vlo.init(lane);
-  DirectLoader<GK, 4> kld;
+  DirectLoader<GK, kDqWaves> kld;
   kld.init(p.skt, p.D, wave, lane);
-  DirectLoader<GV, 4> vld;
+  DirectLoader<GV, kDqWaves> vld;
   vld.init(p.skt, p.D, wave, lane);
 
   f32x16 dq[DBLK];
@@ -983,14 +992,14 @@ HARP_RA_INSTANTIATE(8, 4)
 // ---------------------------------------------------------------------------
 template <int KSTEPS, int DBLK>
 static hipError_t launch_fwd_t(const FwdParams& p, hipStream_t st) {
-  const int n = ((p.T + 127) / 128) * p.H * p.B;
-  hipLaunchKernelGGL((fwd_kernel<KSTEPS, DBLK>), dim3(n), dim3(256), 0, st, p);
+  const int n = ((p.T + kFwdRows - 1) / kFwdRows) * p.H * p.B;
+  hipLaunchKernelGGL((fwd_kernel<KSTEPS, DBLK>), dim3(n), dim3(64 * kFwdWaves), 0, st, p);
   return hipGetLastError();
 }
 template <int KSTEPS, int DBLK>
 static hipError_t launch_dq_t(const BwdParams& p, hipStream_t st) {
-  const int n = ((p.T + 127) / 128) * p.H * p.B;
-  hipLaunchKernelGGL((dq_kernel<KSTEPS, DBLK>), dim3(n), dim3(256), 0, st, p);
+  const int n = ((p.T + kDqRows - 1) / kDqRows) * p.H * p.B;
+  hipLaunchKernelGGL((dq_kernel<KSTEPS, DBLK>), dim3(n), dim3(64 * kDqWaves), 0, st, p);
   return hipGetLastError();
 }
 template <int KSTEPS, int DBLK>
