@@ -303,3 +303,29 @@ def test_returns_alias_inputs():
     l = torch.empty((1, 4, 200, 1), device="cuda", dtype=torch.float32)
     r = torch.ops.ring_attention_ops.ring_attention_forward(qd, kd, vd, out, m, l, 3, scale)
     assert r[0].data_ptr() == out.data_ptr() and r[1].data_ptr() == m.data_ptr() and r[2].data_ptr() == l.data_ptr()
+
+
+# --- every head-dim variant -----------------------------------------------------
+
+@pytest.mark.parametrize("D", [8, 16, 24, 32, 40, 48, 56, 64, 72, 80, 88, 96, 104, 112, 120, 128])
+def test_head_dim_sweep(D):
+    """Every kernel variant the launchers dispatch to (D <= 32, 64, 72, <= 96,
+    128) and every padding case inside them (D below the variant's tile
+    width), on a small ragged problem against the full fp64 oracle."""
+    q, ks, vs, do = orc.make_inputs(1, 2, 150, D, 2, seed=100 + D, chunk_len=97)
+    scale = 1.0 / math.sqrt(D)
+    print(f"[head dim D={D}]", flush=True)
+    res = run_hip(q, ks, vs, do, scale)
+    ref = _oracle_full(q, ks, vs, do, scale)
+    _check_all(res, ref)
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_config2_robustness_seeds(seed):
+    """Config 2 (B1 H16 T2048 D64, 4 chunks) with the robustness seeds, every
+    element against the fp32 oracle."""
+    q, ks, vs, do = orc.make_inputs(1, 16, 2048, 64, 4, seed=seed, chunk_len=2048)
+    print(f"[config 2 seed {seed}]", flush=True)
+    res = run_hip(q, ks, vs, do, 0.125)
+    ref = _oracle_full(q, ks, vs, do, 0.125, dtype=torch.float32)
+    _check_all(res, ref)
