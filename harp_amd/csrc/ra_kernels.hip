@@ -364,10 +364,12 @@ __device__ __forceinline__ void decode_block(int n_tiles, int H, int& tile, int&
   b = bh / H;
 }
 
-// Next (ring step, key tile) after (step, k0), skipping empty chunks.
-__device__ __forceinline__ void next_tile(const ChunkTable& ct, int step, int k0, int& nstep, int& nk0) {
+// Next (ring step, first key) after the tile of tile_keys keys at (step, k0),
+// skipping empty chunks.
+__device__ __forceinline__ void next_tile(const ChunkTable& ct, int step, int k0, int tile_keys, int& nstep,
+                                          int& nk0) {
   nstep = step;
-  nk0 = k0 + 64;
+  nk0 = k0 + tile_keys;
   while (nstep < ct.n && nk0 >= ct.len[ct.order[nstep]]) {
     ++nstep;
     nk0 = 0;
@@ -382,17 +384,24 @@ __device__ __forceinline__ void next_tile(const ChunkTable& ct, int step, int k0
 // writes per MFMA against two 4-wave blocks per CU.
 constexpr int kFwdWaves = 8;
 constexpr int kFwdRows = 32 * kFwdWaves;
+// Keys per tile = 64 * kFwdSub: fewer barriers, pipeline fills and row-max
+// passes per key; the block's LDS holds two such K / V tiles.
+#ifndef HARP_FWD_SUB
+#define HARP_FWD_SUB 2
+#endif
+constexpr int kFwdSub = HARP_FWD_SUB;
 // KSTEPS = ceil(D/16) k-steps of the S contraction; DBLK = ceil(D/32) row
 // blocks of O^T (DP = 32*DBLK >= 16*KSTEPS).  Block = kFwdWaves waves x 32 queries;
-// 64-key tiles.
+// 64*kFwdSub-key tiles (kFwdSub 64-row LDS sub-tiles).
 template <int KSTEPS, int DBLK>
 __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
   constexpr int DP = DBLK * 32;
   using GK = PadTile<DP>;  // K: row fragments only
   using GV = XorTile<DP>;  // V: transposed fragments
   constexpr float kTau = 8.f;  // lazy-rescale threshold (log2 units): P <= 2^8
-  __shared__ __attribute__((aligned(16))) bf16 Ks[2][GK::ELEMS];
-  __shared__ __attribute__((aligned(16))) bf16 Vs[2][GV::ELEMS];
+  constexpr int NS = kFwdSub, KB = 2 * NS;  // 64-row sub-tiles, 32-key blocks per tile
+  __shared__ __attribute__((aligned(16))) bf16 Ks[2][NS][GK::ELEMS];
+  __shared__ __attribute__((aligned(16))) bf16 Vs[2][NS][GV::ELEMS];
 
   // the wave index is wave-uniform; readfirstlane lets the compiler keep it in an SGPR
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -431,9 +440,12 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
   const int64_t kvo = (int64_t)b * p.skb + (int64_t)h * p.skh;
   auto issue = [&](int step, int k0, int bf) {
     const int c = p.ct.order[step];
-    const int rows = p.ct.len[c] - k0;
-    kld.load(rows_rsrc(p.ct.k[c] + kvo, p.skt, k0, rows), Ks[bf]);
-    vld.load(rows_rsrc(p.ct.v[c] + kvo, p.skt, k0, rows), Vs[bf]);
+#pragma unroll
+    for (int sb = 0; sb < NS; ++sb) {
+      const int r0 = k0 + 64 * sb, rows = p.ct.len[c] - r0;
+      kld.load(rows_rsrc(p.ct.k[c] + kvo, p.skt, r0, rows), Ks[bf][sb]);
+      vld.load(rows_rsrc(p.ct.v[c] + kvo, p.skt, r0, rows), Vs[bf][sb]);
+    }
   };
   int step = 0, k0 = 0;
   while (step < p.ct.n && p.ct.len[p.ct.order[step]] == 0) ++step;
@@ -445,25 +457,22 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
   while (step < p.ct.n) {
     const int kv_left = p.ct.len[p.ct.order[step]] - k0;
     int nstep, nk0;
-    next_tile(p.ct, step, k0, nstep, nk0);
+    next_tile(p.ct, step, k0, 64 * NS, nstep, nk0);
     wait_lds_loads();
     __syncthreads();
     if (nstep < p.ct.n) issue(nstep, nk0, buf ^ 1);
-    const bf16* K = Ks[buf];
-    const bf16* V = Vs[buf];
-
-    // S^T (keys x queries), two 32-key blocks; step i = (ks = i/2, kb = i%2)
-    f32x16 s[2];
-    s[0] = zero16();
-    s[1] = zero16();
-    pipelined<2 * KSTEPS, 2>([&](int i) { return klo.frag(K, i & 1, i >> 1); },
-                             [&](int i, const bf16x8& a) { s[i & 1] = mfma32x32x16(a, qf[i >> 1], s[i & 1]); });
-    if (kv_left < 64) {  // tail tile of a chunk: mask keys past its valid length
+    // S^T (keys x queries), KB 32-key blocks; step i = (ks = i / KB, kb = i % KB)
+    f32x16 s[KB];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) s[kb] = zero16();
+    pipelined<KB * KSTEPS, 2>([&](int i) { return klo.frag(Ks[buf][(i % KB) / 2], i & 1, i / KB); },
+                              [&](int i, const bf16x8& a) { s[i % KB] = mfma32x32x16(a, qf[i / KB], s[i % KB]); });
+    if (kv_left < 64 * NS) {  // tail tile of a chunk: mask keys past its valid length
       // a side-effecting (empty) asm keeps this a real uniform branch instead
       // of selects that would run on every tile
       asm volatile("");
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int r = 0; r < 16; ++r)
           if (kb * 32 + c_row(r, g) >= kv_left) s[kb][r] = -INFINITY;
@@ -472,7 +481,7 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
     // online softmax, lane = query
     float mx = -INFINITY;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
     mx = wave_half_max(mx) * c2;
@@ -489,9 +498,9 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
     }
     const float m_use = (m_ref == -INFINITY) ? 0.f : m_ref;
 
-    bf16x8 pf[4];
+    bf16x8 pf[2 * KB];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
@@ -501,11 +510,10 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
           pf[kb * 2 + hf][j] = (bf16)e;
         }
 
-    // O^T += V^T P^T; step i = (ks2 = i / DBLK, db = i % DBLK)
-    pipelined<4 * DBLK, 2>([&](int i) { return vlo.tr_frag(V, (i / DBLK) * 16, i % DBLK); },
-                           [&](int i, const bf16x8& a) {
-                             o[i % DBLK] = mfma32x32x16(a, pf[i / DBLK], o[i % DBLK]);
-                           });
+    // O^T += V^T P^T; step i = (ks2 = i / DBLK, db = i % DBLK), 16 keys per ks2
+    pipelined<2 * KB * DBLK, 2>(
+        [&](int i) { return vlo.tr_frag(Vs[buf][(i / DBLK) / 4], ((i / DBLK) % 4) * 16, i % DBLK); },
+        [&](int i, const bf16x8& a) { o[i % DBLK] = mfma32x32x16(a, pf[i / DBLK], o[i % DBLK]); });
 
     buf ^= 1;
     step = nstep;
@@ -651,7 +659,7 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
 #pragma unroll 1
   while (step < p.ct.n) {
     int nstep, nk0;
-    next_tile(p.ct, step, k0, nstep, nk0);
+    next_tile(p.ct, step, k0, 64, nstep, nk0);
     wait_lds_loads();
     __syncthreads();
     if (nstep < p.ct.n) issue(nstep, nk0, buf ^ 1);
