@@ -430,7 +430,7 @@ int harp_ra_backward(const void* q, const int64_t* q_strides, void* grad_q, cons
     p.ct.order[c] = (c + ring_rank) % sp_size;
     p.ct.tile0[c] = key_tiles;
     p.ct_rows[c] = kv_chunk_len;
-    key_tiles += (kv_chunk_len + 127) / 128;
+    key_tiles += (kv_chunk_len + kDkdvBlockKeys - 1) / kDkdvBlockKeys;
   }
   p.n_key_tiles = key_tiles;
   if ((int64_t)key_tiles * h_num * batch > INT32_MAX || (int64_t)((t_num + 127) / 128) * h_num * batch > INT32_MAX)

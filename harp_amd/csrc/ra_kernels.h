@@ -46,12 +46,15 @@ struct BwdParams {
   int m_bf16;
   const float* l;
   const float* delta;
-  int n_key_tiles;          // 128-key tiles per (b, h) over all chunks
+  int n_key_tiles;          // kDkdvBlockKeys-key blocks per (b, h) over all chunks
   int ct_rows[kMaxChunks];  // stored rows of chunk c (dK/dV rows written, pads get 0)
   int B, H, T, D;
   float scale;
   ChunkTable ct;
 };
+
+// Keys per dK/dV block (the host sizes the grid and the chunk table with it).
+constexpr int kDkdvBlockKeys = 256;
 
 hipError_t launch_fwd(const FwdParams& p, hipStream_t st);
 hipError_t launch_delta(const DeltaParams& p, hipStream_t st);

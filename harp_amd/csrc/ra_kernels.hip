@@ -10,7 +10,7 @@
 //                 -> O^T += V^T P^T, over every 64-key tile of every chunk in ring order.
 //   delta_kernel  D = rowsum(dO * O) (fp32).
 //   dq_kernel     per 256-query tile: recompute S^T, dP^T, dS^T; dQ^T += K^T dS^T.
-//   dkdv_kernel   per 128-key tile (KV-stationary like the reference): per 64-query
+//   dkdv_kernel   per 256-key block (KV-stationary like the reference): per 64-query
 //                 tile recompute S, dP; dV += P^T dO, dK += dS^T Q.
 //
 // Memory path: every streamed 64-row tile is copied global -> LDS by
@@ -237,6 +237,44 @@ struct XorLanes {
   __device__ __forceinline__ bf16x8 row_frag(const bf16* t, int rb, int ks) const {
     return *(const bf16x8*)(t + rb * 32 * G::W + row_off[ks]);
   }
+  // the same row fragment from two per-lane registers (row base and
+  // swizzle) instead of KSTEPS offsets: (2ks + g) ^ swz(l32) = 2ks ^ (g ^ swz(l32))
+  int row_base, row_x;
+  // transposed reads from NDB offsets plus one per-lane delta: the hh = 1
+  // offset differs from hh = 0 by 8 rows and by flipping bit 1 of the chunk
+  // index, the same for every db
+  int tr_lean[NDB], tr_delta;
+  __device__ __forceinline__ void init_tr_lean(int lane) {
+    const int g = lane >> 5, j = lane >> 4, s = (lane >> 2) & 3, m = lane & 3;
+    const int cl = 2 * (j & 1) + (m >> 1);
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      const int row = 4 * g + s;
+      tr_lean[db] = row * G::W + (((4 * db + cl) ^ swz(row)) << 3) + 4 * (m & 1);
+    }
+    const int row1 = 8 + 4 * g + s;
+    tr_delta = row1 * G::W + (((cl) ^ swz(row1)) << 3) - ((4 * g + s) * G::W + (((cl) ^ swz(4 * g + s)) << 3));
+  }
+  __device__ __forceinline__ bf16x8 tr_frag_lean(const bf16* t, int r0, int db) const {
+    const bf16* p0 = t + r0 * G::W + tr_lean[db];
+    const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p0);
+    const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p0 + tr_delta));
+    bf16x8 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      r[i] = lo[i];
+      r[i + 4] = hi[i];
+    }
+    return r;
+  }
+  __device__ __forceinline__ void init_rows_lean(int lane) {
+    const int l32 = lane & 31, g = lane >> 5;
+    row_base = l32 * G::W;
+    row_x = g ^ swz(l32);
+  }
+  __device__ __forceinline__ bf16x8 row_frag_lean(const bf16* t, int rb, int ks) const {
+    return *(const bf16x8*)(t + rb * 32 * G::W + row_base + (((2 * ks) ^ row_x) << 3));
+  }
   // k-operand fragment read transposed: T[r0 + {4g+0..3, 8+4g+0..3}][32*db + l32]
   // ds_read_b64_tr_b16: in each 16-lane group, lane i slot s' receives element
   // i%4 of the 8 bytes addressed by lane 4s' + i/4 of that group.
@@ -311,6 +349,9 @@ __device__ __forceinline__ void pipelined(const Load& load, const Mma& mma) {
 
 struct Frag2 {
   bf16x8 a, b;
+};
+struct Frag3 {
+  bf16x8 a, b, c;
 };
 
 // DPP row_newbcast:R -- every lane of each 16-lane row receives lane R of
@@ -717,33 +758,34 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
 // ---------------------------------------------------------------------------
 // Backward dK/dV (KV-stationary, as ring_attn.cpp:2723-2816)
 // ---------------------------------------------------------------------------
-// Block = 4 waves x 32 keys.  The block's 128 K and V rows are copied to LDS
-// once and each wave keeps its 32 rows as MFMA B operands in registers; the
-// loop streams 64-query tiles of Q / dO (+ per-query LSE and D) through
-// double-buffered LDS and handles each tile as two 32-query halves.  Per half:
-//   A: S = Q K^T, dP = dO V^T          (MFMA; C row = query, col = key)
-//   B: P = exp2(S c - LSE2), dS = P (dP - D)        (VALU)
-//   C: dV += P^T dO, dK += dS^T Q      (MFMA; dO^T / Q^T read transposed)
-// One wave per SIMD, so the VALU work of B is hidden by interleaving it, a
-// pair of elements at a time, between the MFMAs of a neighbouring phase:
-//   tile t:  A(t,0)  ->  A(t,1) | B(t,0)  ->  C(t,0) | B(t,1)  ->  C(t,1)  ->  barrier
-// The barrier publishes tile t+1 and frees tile t's buffer for tile t+2's
-// loads, which then complete under a whole tile of MFMA work.
+// Block = 8 waves x 32 keys (256 keys; two waves per SIMD, one block per CU).
+// Each wave keeps its 32 K rows as MFMA B operands in registers and reads
+// its V rows from the block's LDS copy; dK, dV accumulate in fp32 AGPRs over
+// every query.  Queries stream in 64-row tiles (Q, dO, per-row LSE2 and D)
+// through double-buffered LDS; per 32-query half:
+//   A: S = Q K^T, dP = dO V^T      (C row = query, col = key)
+//   B: P = exp2(S c - LSE2), dS = P (dP - D)
+//   C: dV += P^T dO, dK += dS^T Q  (P / dS straight from the accumulator
+//      layout as A operands; dO^T, Q^T by transposed LDS reads)
+// Two waves per SIMD hide each other's VALU and LDS latency, and one LDS
+// wave can only keep ~16 reads in flight: at two waves a SIMD gets ~1.5x the
+// LDS read throughput of one.  Each Q / dO tile in LDS serves 256 keys.
 // Pad keys (past the chunk's valid length) are written as zero at the end
 // instead of being masked per tile: a key's P / dS only reach its own dK / dV.
+constexpr int kDkWaves = kDkdvBlockKeys / 32;
 template <int KSTEPS, int DBLK>
-__global__ __launch_bounds__(256, 1) void dkdv_kernel(BwdParams p) {
+__global__ __launch_bounds__(64 * kDkWaves, 1) void dkdv_kernel(BwdParams p) {
   constexpr int DP = DBLK * 32;
-  using GK = PadTile<DP>;  // the block's K / V rows: row fragments only
+  using GV = PadTile<DP>;  // the block's V rows: row fragments only
   using GQ = XorTile<DP>;  // Q / dO tiles: row and transposed fragments
-  constexpr int NPAIR = 8;  // element pairs of B per half (16 C registers)
-  __shared__ __attribute__((aligned(16))) bf16 Kb[2 * GK::ELEMS];  // 128 key rows
-  __shared__ __attribute__((aligned(16))) bf16 Vb[2 * GK::ELEMS];
-  __shared__ __attribute__((aligned(16))) bf16 Qs[2][GQ::ELEMS];
-  __shared__ __attribute__((aligned(16))) bf16 Gs[2][GQ::ELEMS];
-  __shared__ __attribute__((aligned(16))) float St[2][128];  // per query: (LSE2, D)
+  constexpr int NVT = kDkdvBlockKeys / 64;  // 64-row V tiles of the block
+  __shared__ __attribute__((aligned(16))) bf16 Vb[NVT][GV::ELEMS];
+  // two Q / dO buffers; before the loop they hold the block's K rows (as
+  // NVT XorTiles) while each wave copies its K fragments into registers
+  __shared__ __attribute__((aligned(16))) bf16 QG[2][2][GQ::ELEMS];  // [buffer][Q, dO]
+  __shared__ __attribute__((aligned(16))) float St[2][128];            // per query: (LSE2, D)
+  static_assert(NVT <= 4, "K staging uses the four Q / dO tile slots");
 
-  // the wave index is wave-uniform; readfirstlane lets the compiler keep it in an SGPR
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, g = lane >> 5;
   int kt, h, b;
@@ -752,7 +794,7 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(BwdParams p) {
 #pragma unroll 1
   for (int i = 1; i < p.ct.n; ++i)
     if (kt >= p.ct.tile0[i]) c = i;
-  const int kblk0 = (kt - p.ct.tile0[c]) * 128;
+  const int kblk0 = (kt - p.ct.tile0[c]) * kDkdvBlockKeys;
   const int key0 = kblk0 + wave * 32;
   const int len = p.ct.len[c];
   const float c2 = p.scale * kLog2e;
@@ -762,91 +804,73 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(BwdParams p) {
   for (int i = 0; i < DBLK; ++i) {
     dk[i] = zero16();
     dv[i] = zero16();
-    pin_agpr(dk[i]);
-    pin_agpr(dv[i]);
   }
 
   if (kblk0 < len) {  // block has at least one valid key (block-uniform)
     XorLanes<DP, KSTEPS> lo;
-    lo.init(lane);
-    StagedLoader<GQ, 4> qld, gld;
+    lo.init_rows_lean(lane);
+    lo.init_tr_lean(lane);
+    PadRows<DP> vlo;
+    vlo.init(lane);
+    DirectLoader<GQ, kDkWaves> qld, gld;
     qld.init(p.sqt, p.D, wave, lane);
     gld.init(p.sdt, p.D, wave, lane);
     const bf16* qb_ = p.q + (int64_t)b * p.sqb + (int64_t)h * p.sqh;
     const bf16* gb_ = p.dout + (int64_t)b * p.sdb + (int64_t)h * p.sdh;
     const int64_t sbase = ((int64_t)b * p.H + h) * p.T;
 
-    // Q / dO tiles are fetched into registers two tiles ahead (two register
-    // sets alternate, so a fetch has two tiles of work to complete) and are
-    // written to the idle LDS buffer during the last MFMA phase of the tile
-    // before the one that reads them; the barrier that ends that tile
-    // publishes them.  Per-query statistics ride along: wave 0 loads the raw
-    // m / l / D bits with the tile and converts them only when it stores
-    // them, so no wave stalls on these loads' latency.
-    using QData = typename StagedLoader<GQ, 4>::Data;
-    QData qdat[2], gdat[2];
-    uint32_t m_bits[2] = {0, 0}, l_bits[2] = {0, 0}, d_bits[2] = {0, 0};
-    auto fetch_tile = [&](auto setc, int q0) {
-      constexpr int S = decltype(setc)::value;
-      qld.fetch(qdat[S], qb_ + (int64_t)q0 * p.sqt, (uint32_t)((int64_t)(p.T - q0) * p.sqt * 2));
-      gld.fetch(gdat[S], gb_ + (int64_t)q0 * p.sdt, (uint32_t)((int64_t)(p.T - q0) * p.sdt * 2));
+    // Per-query statistics of the next tile: wave 0 loads the raw m / l / D
+    // bits when it issues the tile and converts them only in store_stats,
+    // after the wait that precedes the barrier.
+    uint32_t m_bits = 0, l_bits = 0, d_bits = 0;
+    auto issue = [&](int q0, int bf) {
+      qld.load(rows_rsrc(qb_, p.sqt, q0, p.T - q0), QG[bf][0]);
+      gld.load(rows_rsrc(gb_, p.sdt, q0, p.T - q0), QG[bf][1]);
       if (tid < 64) {
         const int qq = q0 + tid;
-        m_bits[S] = l_bits[S] = d_bits[S] = 0;  // l = 0 marks a row past T: P = 0
+        m_bits = l_bits = d_bits = 0;  // l = 0 marks a row past T: P = 0
         if (qq < p.T) {
           const int64_t i = sbase + qq;
-          m_bits[S] = p.m_bf16 ? (uint32_t)((const uint16_t*)p.m)[i] : ((const uint32_t*)p.m)[i];
-          l_bits[S] = ((const uint32_t*)p.l)[i];
-          d_bits[S] = ((const uint32_t*)p.delta)[i];
+          m_bits = p.m_bf16 ? (uint32_t)((const uint16_t*)p.m)[i] : ((const uint32_t*)p.m)[i];
+          l_bits = ((const uint32_t*)p.l)[i];
+          d_bits = ((const uint32_t*)p.delta)[i];
         }
       }
     };
-    constexpr int kQI = StagedLoader<GQ, 4>::kInst;
-    // slot j of set S (Q slots, then dO slots) into LDS buffer bf
-    auto store_slot = [&](auto setc, int bf, int j) {
-      constexpr int S = decltype(setc)::value;
-      if (j < kQI) qld.store_one(qdat[S], Qs[bf], j);
-      else gld.store_one(gdat[S], Gs[bf], j - kQI);
-    };
-    auto store_stats = [&](auto setc, int bf) {
-      constexpr int S = decltype(setc)::value;
+    auto store_stats = [&](int bf) {
       if (tid < 64) {
-        const float mm = __uint_as_float(p.m_bf16 ? m_bits[S] << 16 : m_bits[S]);
-        const float ll = __uint_as_float(l_bits[S]);
+        const float mm = __uint_as_float(p.m_bf16 ? m_bits << 16 : m_bits);
+        const float ll = __uint_as_float(l_bits);
         const float lse2 = (ll > 0.f) ? (mm + __logf(ll)) * kLog2e : INFINITY;
-        *(float2*)&St[bf][2 * tid] = make_float2(lse2, __uint_as_float(d_bits[S]));
+        *(float2*)&St[bf][2 * tid] = make_float2(lse2, __uint_as_float(d_bits));
       }
     };
 
-    bf16x8 kf[KSTEPS], vf[KSTEPS];
+    bf16x8 kf[KSTEPS];
     {
-      DirectLoader<GK, 4> kvl;
-      kvl.init(p.skt, p.D, wave, lane);
       const int64_t kvo = (int64_t)b * p.skb + (int64_t)h * p.skh;
+      DirectLoader<GQ, kDkWaves> kld;
+      kld.init(p.skt, p.D, wave, lane);
+      DirectLoader<GV, kDkWaves> vld;
+      vld.init(p.skt, p.D, wave, lane);
+      bf16* kstage = &QG[0][0][0];
 #pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        const int r0 = kblk0 + 64 * half;
-        kvl.load(rows_rsrc(p.ct.k[c] + kvo, p.skt, r0, len - r0), Kb + half * GK::ELEMS);
-        kvl.load(rows_rsrc(p.ct.v[c] + kvo, p.skt, r0, len - r0), Vb + half * GK::ELEMS);
+      for (int t = 0; t < NVT; ++t) {
+        const int r0 = kblk0 + 64 * t;
+        kld.load(rows_rsrc(p.ct.k[c] + kvo, p.skt, r0, len - r0), kstage + t * GQ::ELEMS);
+        vld.load(rows_rsrc(p.ct.v[c] + kvo, p.skt, r0, len - r0), Vb[t]);
       }
-      fetch_tile(Int<0>{}, 0);
-#pragma unroll
-      for (int j = 0; j < 2 * kQI; ++j) store_slot(Int<0>{}, 0, j);
-      store_stats(Int<0>{}, 0);
       wait_lds_loads();
       __syncthreads();
-      // this wave's 32 K / V rows as MFMA B operands for the whole loop
-      PadRows<DP> klo;
-      klo.init(lane);
+      // this wave's 32 K rows: XorTile wave / 2, 32-row block wave % 2
 #pragma unroll
-      for (int ks = 0; ks < KSTEPS; ++ks) {
-        kf[ks] = klo.frag(Kb, wave, ks);
-        vf[ks] = klo.frag(Vb, wave, ks);
-      }
+      for (int ks = 0; ks < KSTEPS; ++ks) kf[ks] = lo.row_frag_lean(kstage + (wave >> 1) * GQ::ELEMS, wave & 1, ks);
+      __syncthreads();  // every wave has its K fragments: the staging may be overwritten
     }
-    const int n_tiles = (p.T + 63) >> 6;
-    if (n_tiles > 1) fetch_tile(Int<1>{}, 64);
-    if (n_tiles > 2) fetch_tile(Int<0>{}, 128);
+    const bf16* Vw = Vb[wave >> 1];
+    const int vrb = wave & 1;
+    issue(0, 0);
+    store_stats(0);  // (waits for wave 0's statistics loads)
 
     // (LSE2, D) of query row c_row(lane % 16, g) of half qb: one read per lane
     // per half; row_bcast then hands each C register r the values of its own
@@ -854,105 +878,48 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(BwdParams p) {
     auto stats_lane = [&](int bf, int qb) {
       return *(const float2*)&St[bf][2 * (qb * 32 + c_row(lane & 15, g))];
     };
-    // B for element pair j (C registers 2j, 2j+1) of one half
-    auto pds_pair = [&](const f32x16& s, const f32x16& dp, int j, const float2& st, bf16x8* pf, bf16x8* dsf) {
-      const int r = 2 * j;
-      const float p0 = fast_exp2(__builtin_fmaf(s[r], c2, -row_bcast(st.x, r)));
-      const float p1 = fast_exp2(__builtin_fmaf(s[r + 1], c2, -row_bcast(st.x, r + 1)));
-      pf[r >> 3][r & 7] = (bf16)p0;
-      pf[r >> 3][(r & 7) + 1] = (bf16)p1;
-      dsf[r >> 3][r & 7] = (bf16)(p0 * (dp[r] - row_bcast(st.y, r)));
-      dsf[r >> 3][(r & 7) + 1] = (bf16)(p1 * (dp[r + 1] - row_bcast(st.y, r + 1)));
-    };
-    // One 64-query tile t; S = t % 2 names its LDS buffer and the register
-    // set that holds tile t + 1 is 1 - S (compile-time, so the register sets
-    // are never indexed dynamically).  Returns true after the last tile.
-    auto tile = [&](auto setc, int t) -> bool {
-      constexpr int S = decltype(setc)::value;
-      const bf16* Q = Qs[S];
-      const bf16* Gd = Gs[S];
-#pragma unroll
-      for (int i = 0; i < DBLK; ++i) {
-        pin_agpr(dk[i]);
-        pin_agpr(dv[i]);
-      }
-      f32x16 s0 = zero16(), dp0 = zero16(), s1 = zero16(), dp1 = zero16();
-      bf16x8 pf0[2], dsf0[2], pf1[2], dsf1[2];
-      const float2 st0 = stats_lane(S, 0), st1 = stats_lane(S, 1);
-      // The tile's four phases run as one software pipeline of
-      // 2*KSTEPS + 4*DBLK steps (two MFMAs each), so the fragments of a
-      // phase's first steps are in flight while the previous phase finishes:
-      //   [0, SA)              A(t,0)
-      //   [SA, 2SA)            A(t,1) | B(t,0)
-      //   [2SA, 2SA+SC)        C(t,0) | B(t,1)
-      //   [2SA+SC, 2SA+2SC)    C(t,1) | tile t+1 registers -> LDS buffer 1-S
-      // (buffer 1-S held tile t-1, which every wave finished before the
-      // barrier that ended tile t-1; past the last tile the stores are unused)
-      constexpr int SA = KSTEPS, SC = 2 * DBLK, NST = 2 * kQI;
-      pipelined<2 * SA + 2 * SC, 2>(
-          [&](auto ii) {
-            constexpr int i = decltype(ii)::value;
-            if constexpr (i < 2 * SA) {
-              return Frag2{lo.row_frag(Q, i / SA, i % SA), lo.row_frag(Gd, i / SA, i % SA)};
-            } else {
-              constexpr int c = i - 2 * SA, st = c % SC, r0 = (c / SC) * 32 + (st / DBLK) * 16;
-              return Frag2{lo.tr_frag(Gd, r0, st % DBLK), lo.tr_frag(Q, r0, st % DBLK)};
-            }
-          },
-          [&](auto ii, const Frag2& f) {
-            constexpr int i = decltype(ii)::value;
-            if constexpr (i < SA) {
-              s0 = mfma32x32x16(f.a, kf[i], s0);
-              dp0 = mfma32x32x16(f.b, vf[i], dp0);
-            } else if constexpr (i < 2 * SA) {
-              constexpr int ks = i - SA;
-              const int j0 = ks * NPAIR / SA, j1 = (ks + 1) * NPAIR / SA, jm = (j0 + j1 + 1) / 2;
-              s1 = mfma32x32x16(f.a, kf[ks], s1);
-              sched_fence();
-#pragma unroll
-              for (int j = j0; j < jm; ++j) pds_pair(s0, dp0, j, st0, pf0, dsf0);
-              sched_fence();
-              dp1 = mfma32x32x16(f.b, vf[ks], dp1);
-              sched_fence();
-#pragma unroll
-              for (int j = jm; j < j1; ++j) pds_pair(s0, dp0, j, st0, pf0, dsf0);
-            } else if constexpr (i < 2 * SA + SC) {
-              constexpr int st = i - 2 * SA, h2 = st / DBLK, db = st % DBLK;
-              const int j0 = st * NPAIR / SC, j1 = (st + 1) * NPAIR / SC, jm = (j0 + j1 + 1) / 2;
-              dv[db] = mfma32x32x16(pf0[h2], f.a, dv[db]);
-              sched_fence();
-#pragma unroll
-              for (int j = j0; j < jm; ++j) pds_pair(s1, dp1, j, st1, pf1, dsf1);
-              sched_fence();
-              dk[db] = mfma32x32x16(dsf0[h2], f.b, dk[db]);
-              sched_fence();
-#pragma unroll
-              for (int j = jm; j < j1; ++j) pds_pair(s1, dp1, j, st1, pf1, dsf1);
-            } else {
-              constexpr int st = i - 2 * SA - SC, h2 = st / DBLK, db = st % DBLK;
-              dv[db] = mfma32x32x16(pf1[h2], f.a, dv[db]);
-              sched_fence();
-#pragma unroll
-              for (int j = st * NST / SC; j < (st + 1) * NST / SC; ++j) store_slot(Int<1 - S>{}, 1 - S, j);
-              sched_fence();
-              dk[db] = mfma32x32x16(dsf1[h2], f.b, dk[db]);
-            }
-          });
-#pragma unroll
-      for (int i = 0; i < DBLK; ++i) {
-        pin_agpr(dk[i]);
-        pin_agpr(dv[i]);
-      }
-      if (t + 1 >= n_tiles) return true;
-      store_stats(Int<1 - S>{}, 1 - S);
-      __syncthreads();  // tile t+1 published; every wave is done with tile t
-      if (t + 3 < n_tiles) fetch_tile(Int<1 - S>{}, (t + 3) * 64);
-      return false;
-    };
+    const int n_tiles = (p.T + 63) >> 6;
+    int buf = 0;
 #pragma unroll 1
-    for (int t = 0;; t += 2) {
-      if (tile(Int<0>{}, t)) break;
-      if (tile(Int<1>{}, t + 1)) break;
+    for (int t = 0; t < n_tiles; ++t) {
+      wait_lds_loads();
+      __syncthreads();  // tile t published; every wave is done with tile t-1
+      if (t + 1 < n_tiles) issue((t + 1) * 64, buf ^ 1);
+      const bf16* Q = QG[buf][0];
+      const bf16* Gd = QG[buf][1];
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        const float2 st = stats_lane(buf, qb);
+        f32x16 s = zero16(), dp = zero16();
+        pipelined<KSTEPS, 1>(
+            [&](int ks) { return Frag2{lo.row_frag_lean(Q, qb, ks), lo.row_frag_lean(Gd, qb, ks)}; },
+            [&](int ks, const Frag2& f) {
+              const bf16x8 v = vlo.frag(Vw, vrb, ks);
+              s = mfma32x32x16(f.a, kf[ks], s);
+              dp = mfma32x32x16(f.b, v, dp);
+            });
+        bf16x8 pf[2], dsf[2];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float pv = fast_exp2(__builtin_fmaf(s[r], c2, -row_bcast(st.x, r)));
+          pf[r >> 3][r & 7] = (bf16)pv;
+          dsf[r >> 3][r & 7] = (bf16)(pv * (dp[r] - row_bcast(st.y, r)));
+        }
+        // dV += P^T dO ; dK += dS^T Q (M = keys, N = d, K = the 32 queries of
+        // this half); step s2 = (h2 = s2 / DBLK, db = s2 % DBLK)
+        pipelined<2 * DBLK, 1>(
+            [&](int s2) {
+              const int r0 = qb * 32 + (s2 / DBLK) * 16;
+              return Frag2{lo.tr_frag_lean(Gd, r0, s2 % DBLK), lo.tr_frag_lean(Q, r0, s2 % DBLK)};
+            },
+            [&](int s2, const Frag2& f) {
+              const int h2 = s2 / DBLK, db = s2 % DBLK;
+              dv[db] = mfma32x32x16(pf[h2], f.a, dv[db]);
+              dk[db] = mfma32x32x16(dsf[h2], f.b, dk[db]);
+            });
+      }
+      if (t + 1 < n_tiles) store_stats(buf ^ 1);
+      buf ^= 1;
     }
   }
 
@@ -1013,7 +980,7 @@ static hipError_t launch_dq_t(const BwdParams& p, hipStream_t st) {
 template <int KSTEPS, int DBLK>
 static hipError_t launch_dkdv_t(const BwdParams& p, hipStream_t st) {
   const int n = p.n_key_tiles * p.H * p.B;
-  hipLaunchKernelGGL((dkdv_kernel<KSTEPS, DBLK>), dim3(n), dim3(256), 0, st, p);
+  hipLaunchKernelGGL((dkdv_kernel<KSTEPS, DBLK>), dim3(n), dim3(64 * kDkWaves), 0, st, p);
   return hipGetLastError();
 }
 
