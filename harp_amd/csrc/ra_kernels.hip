@@ -631,6 +631,20 @@ __device__ __forceinline__ float lse2_of(const void* m, int m_bf16, const float*
 // the same reason as the forward: each K / V tile in LDS serves 256 queries.
 constexpr int kDqWaves = 8;
 constexpr int kDqRows = 32 * kDqWaves;
+// Keys per barrier interval = 64 * kDqSub (kDqSub 64-row LDS sub-tiles per
+// buffer).  Within an interval the 32-key blocks j = 0 .. 2*kDqSub-1 run as
+// one software pipeline: A(j) = S^T, dP^T of block j; B(j) = its dS^T (VALU);
+// C(j) = dQ^T += K_j^T dS_j^T.  Order A(0), A(1)|B(0), C(0), A(2)|B(1), C(1),
+// ..., B(last), C(last), where X|Y places Y's VALU instructions between X's
+// MFMAs, so only one block's softmax per interval is exposed.
+#ifndef HARP_DQ_SUB
+#define HARP_DQ_SUB 2
+#endif
+constexpr int kDqSub = HARP_DQ_SUB;
+#ifndef HARP_DQ_PFA
+#define HARP_DQ_PFA 1
+#endif
+constexpr int kDqPfA = HARP_DQ_PFA;  // S^T / dP^T fragments issued this many steps ahead
 // Pad keys need no mask here: their K/V rows load as zero, so their dS has
 // no effect on dQ^T = K^T dS^T.
 template <int KSTEPS, int DBLK>
@@ -638,8 +652,9 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
   constexpr int DP = DBLK * 32;
   using GK = XorTile<DP>;  // K: row and transposed fragments
   using GV = PadTile<DP>;  // V: row fragments only
-  __shared__ __attribute__((aligned(16))) bf16 Ks[2][GK::ELEMS];
-  __shared__ __attribute__((aligned(16))) bf16 Vs[2][GV::ELEMS];
+  constexpr int NS = kDqSub, KB = 2 * NS;
+  __shared__ __attribute__((aligned(16))) bf16 Ks[2][NS][GK::ELEMS];
+  __shared__ __attribute__((aligned(16))) bf16 Vs[2][NS][GV::ELEMS];
 
   // the wave index is wave-uniform; readfirstlane lets the compiler keep it in an SGPR
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -666,7 +681,8 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
   const float lse2 = q_ok ? lse2_of(p.m, p.m_bf16, p.l, si) : INFINITY;
   const float dlt = q_ok ? p.delta[si] : 0.f;
   XorLanes<DP, KSTEPS> klo;
-  klo.init(lane);
+  klo.init_rows_lean(lane);
+  klo.init_tr_lean(lane);
   PadRows<DP> vlo;
   vlo.init(lane);
   DirectLoader<GK, kDqWaves> kld;
@@ -681,9 +697,12 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
   const int64_t kvo = (int64_t)b * p.skb + (int64_t)h * p.skh;
   auto issue = [&](int step, int k0, int bf) {
     const int c = p.ct.order[step];
-    const int rows = p.ct.len[c] - k0;
-    kld.load(rows_rsrc(p.ct.k[c] + kvo, p.skt, k0, rows), Ks[bf]);
-    vld.load(rows_rsrc(p.ct.v[c] + kvo, p.skt, k0, rows), Vs[bf]);
+#pragma unroll
+    for (int sb = 0; sb < NS; ++sb) {
+      const int r0 = k0 + 64 * sb, rows = p.ct.len[c] - r0;
+      kld.load(rows_rsrc(p.ct.k[c] + kvo, p.skt, r0, rows), Ks[bf][sb]);
+      vld.load(rows_rsrc(p.ct.v[c] + kvo, p.skt, r0, rows), Vs[bf][sb]);
+    }
   };
   int step = 0, k0 = 0;
   while (step < p.ct.n && p.ct.len[p.ct.order[step]] == 0) ++step;
@@ -700,40 +719,61 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
 #pragma unroll 1
   while (step < p.ct.n) {
     int nstep, nk0;
-    next_tile(p.ct, step, k0, 64, nstep, nk0);
+    next_tile(p.ct, step, k0, 64 * NS, nstep, nk0);
     wait_lds_loads();
     __syncthreads();
     if (nstep < p.ct.n) issue(nstep, nk0, buf ^ 1);
-    const bf16* K = Ks[buf];
-    const bf16* V = Vs[buf];
 
-    // S^T = K Q^T and dP^T = V dO^T; step i = (ks = i/2, kb = i%2)
+    // S^T / dP^T of two 32-key blocks in flight (block j in slot j & 1) and
+    // the bf16 dS^T of the block whose dQ product is next
     f32x16 s[2], dp[2];
+    bf16x8 dsf[2][2];
+    // B(j), rows r0 .. r0+NR-1: dS^T = P^T (dP^T - D), P^T = exp2(S^T c2 - LSE2)
+    auto softmax_rows = [&](int j, int r0, int nr) {
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      s[kb] = zero16();
-      dp[kb] = zero16();
-    }
-    pipelined<2 * KSTEPS, 2>(
-        [&](int i) { return Frag2{klo.row_frag(K, i & 1, i >> 1), vlo.frag(V, i & 1, i >> 1)}; },
-        [&](int i, const Frag2& f) {
-          s[i & 1] = mfma32x32x16(f.a, qf[i >> 1], s[i & 1]);
-          dp[i & 1] = mfma32x32x16(f.b, gf[i >> 1], dp[i & 1]);
-        });
-    bf16x8 dsf[4];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float pv = fast_exp2(__builtin_fmaf(s[kb][r], c2, -lse2_s));
-        dsf[kb * 2 + (r >> 3)][r & 7] = (bf16)(pv * (dp[kb][r] - dlt_s));
+      for (int r = r0; r < r0 + nr; ++r) {
+        const float pv = fast_exp2(__builtin_fmaf(s[j & 1][r], c2, -lse2_s));
+        dsf[j & 1][r >> 3][r & 7] = (bf16)(pv * (dp[j & 1][r] - dlt_s));
       }
-
-    // dQ^T += K^T dS^T; step i = (ks2 = i / DBLK, db = i % DBLK)
-    pipelined<4 * DBLK, 2>([&](int i) { return klo.tr_frag(K, (i / DBLK) * 16, i % DBLK); },
-                           [&](int i, const bf16x8& a) {
-                             dq[i % DBLK] = mfma32x32x16(a, dsf[i / DBLK], dq[i % DBLK]);
-                           });
+    };
+    // A(j), with B(jb) spread over its KSTEPS steps (jb < 0: none)
+    auto phase_a = [&](auto J, auto JB) {
+      constexpr int j = decltype(J)::value, jb = decltype(JB)::value;
+      const bf16* K = Ks[buf][j / 2];
+      const bf16* V = Vs[buf][j / 2];
+      s[j & 1] = zero16();
+      dp[j & 1] = zero16();
+      constexpr int kRowsPerStep = (16 + KSTEPS - 1) / KSTEPS;
+      pipelined<KSTEPS, kDqPfA>(
+          [&](int ks) { return Frag2{klo.row_frag_lean(K, j & 1, ks), vlo.frag(V, j & 1, ks)}; },
+          [&](int ks, const Frag2& f) {
+            s[j & 1] = mfma32x32x16(f.a, qf[ks], s[j & 1]);
+            dp[j & 1] = mfma32x32x16(f.b, gf[ks], dp[j & 1]);
+            if constexpr (jb >= 0) {
+              const int r0 = ks * kRowsPerStep;
+              if (r0 < 16) softmax_rows(jb, r0, (16 - r0 < kRowsPerStep) ? 16 - r0 : kRowsPerStep);
+            }
+          });
+    };
+    // C(j): dQ^T += K_j^T dS_j^T; step i = (16-key half i / DBLK, d block i % DBLK)
+    auto phase_c = [&](auto J) {
+      constexpr int j = decltype(J)::value;
+      const bf16* K = Ks[buf][j / 2];
+      pipelined<2 * DBLK, 2>(
+          [&](int i) { return klo.tr_frag_lean(K, (j & 1) * 32 + (i / DBLK) * 16, i % DBLK); },
+          [&](int i, const bf16x8& a) { dq[i % DBLK] = mfma32x32x16(a, dsf[j & 1][i / DBLK], dq[i % DBLK]); });
+    };
+    phase_a(Int<0>{}, Int<-1>{});
+    phase_a(Int<1>{}, Int<0>{});
+    phase_c(Int<0>{});
+    if constexpr (KB > 2) {
+      phase_a(Int<2>{}, Int<1>{});
+      phase_c(Int<1>{});
+      phase_a(Int<3>{}, Int<2>{});
+      phase_c(Int<2>{});
+    }
+    softmax_rows(KB - 1, 0, 16);
+    phase_c(Int<KB - 1>{});
 
     buf ^= 1;
     step = nstep;
