@@ -220,6 +220,9 @@ def main() -> int:
             if name in kernel_flops:
                 entry["tflops_algorithmic"] = round(kernel_flops[name] / (avg * 1e-3) / 1e12, 1)
             kernels[name] = entry
+    # sustained MFMA rate of this board (register-fed bf16 MFMA stream on
+    # random operands): what the power limit lets any MFMA-bound kernel reach
+    probe_tf, probe_ghz = _lib.probe_mfma_rate(4096, args.seed)
     dom = max((n for n in kernel_flops if n in kernels), key=lambda n: kt[n][0])
     dom_tf = kernels[dom]["tflops_algorithmic"]
     fwd_ms = kt["fwd"][0] / args.steps
@@ -257,6 +260,9 @@ def main() -> int:
             "unit": "TFLOP/s",
             "frac": round(dom_tf / PEAK_BF16_TFLOPS, 4),
             "traffic": MEASURED_TRAFFIC_BYTES.get(args.config, {}).get(dom),
+            "sustained_mfma_tflops": round(probe_tf, 1),
+            "sustained_mfma_shader_ghz": round(probe_ghz, 3),
+            "frac_of_sustained": round(dom_tf / probe_tf, 4) if probe_tf > 0 else None,
         },
         "cpu_baseline": None,
         "gpu": torch.cuda.get_device_name(0),

@@ -60,6 +60,8 @@ ABI_PROTOTYPES = {
     "harp_ra_backward_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i, _i32p]),
     "harp_ra_timing_enable": (_i, [_i]),
     "harp_ra_timing_read": (_i, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int), _i]),
+    "harp_ra_probe_mfma_rate": (_i, [_i, ctypes.c_uint32, ctypes.POINTER(ctypes.c_double),
+                                     ctypes.POINTER(ctypes.c_double)]),
     "harp_ra_last_error": (ctypes.c_char_p, []),
     "harp_ra_version": (ctypes.c_char_p, []),
 }
@@ -119,6 +121,16 @@ def ptr_array(ptrs) -> ctypes.Array:
 
 def i32_array(vals) -> ctypes.Array:
     return (ctypes.c_int32 * len(vals))(*[int(v) for v in vals])
+
+
+def probe_mfma_rate(iters: int = 4096, seed: int = 3407) -> tuple:
+    """(TFLOP/s, shader GHz) of a register-fed bf16 MFMA stream on random
+    operands: the sustained MFMA rate of this device under its power limit."""
+    tf = ctypes.c_double()
+    ghz = ctypes.c_double()
+    check(load_abi().harp_ra_probe_mfma_rate(int(iters), int(seed) & 0xFFFFFFFF, ctypes.byref(tf), ctypes.byref(ghz)),
+          "harp_ra_probe_mfma_rate")
+    return tf.value, ghz.value
 
 
 def timing_enable(on: bool) -> None:

@@ -27,7 +27,7 @@ OUT = ROOT / "kernels"
 ABI_LIB = OUT / "libharp_ra.so"
 OPS_LIB = OUT / "libring_attention_ops.so"
 
-HIP_SOURCES = ["ra_kernels.hip", "ra_abi.hip"]
+HIP_SOURCES = ["ra_kernels.hip", "ra_abi.hip", "ra_probe.hip"]
 HIP_HEADERS = ["ra_common.h", "ra_kernels.h"]
 OPS_SOURCE = "torch_ring_attention_ops.cpp"
 

@@ -245,6 +245,56 @@ int harp_ra_timing_read(double* ms, int* launches, int n_kinds) {
   return ok();
 }
 
+int harp_ra_probe_mfma_rate(int iters, uint32_t seed, double* tflops, double* shader_ghz) {
+  if (!tflops || !shader_ghz) return fail(HARP_RA_EINVAL, "probe outputs are NULL");
+  if (iters < 16 || iters > (1 << 20)) return fail(HARP_RA_EINVAL, "iters=%d must be in [16, 2^20]", iters);
+  int dev = 0, cus = 0, wall_khz = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) ||
+      hipDeviceGetAttribute(&wall_khz, hipDeviceAttributeWallClockRate, dev) || cus < 1 || wall_khz < 1)
+    return fail(HARP_RA_ELAUNCH, "device query failed");
+  const int blocks = 8 * cus;  // 32 waves per CU, 8 per SIMD
+  float* sink = nullptr;
+  long long* clocks = nullptr;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  int rc = HARP_RA_OK;
+  std::vector<long long> h(2 * (size_t)blocks);
+  float best_ms = 0.f;
+  if (hipMalloc(&sink, sizeof(float) * 256 * (size_t)blocks) != hipSuccess ||
+      hipMalloc(&clocks, sizeof(long long) * 2 * (size_t)blocks) != hipSuccess) {
+    rc = fail(HARP_RA_ENOMEM, "probe buffers: hipMalloc failed");
+  } else if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
+    rc = fail(HARP_RA_ELAUNCH, "probe events: hipEventCreate failed");
+  } else {
+    // one warm-up launch (clocks ramp), then the timed one
+    for (int rep = 0; rep < 2 && rc == HARP_RA_OK; ++rep) {
+      (void)hipEventRecord(e0, nullptr);
+      if ((rc = launched(launch_mfma_probe(blocks, iters, seed + (uint32_t)rep, sink, clocks, nullptr), "MFMA probe")))
+        break;
+      (void)hipEventRecord(e1, nullptr);
+      if (hipEventSynchronize(e1) != hipSuccess || hipEventElapsedTime(&best_ms, e0, e1) != hipSuccess)
+        rc = fail(HARP_RA_ELAUNCH, "probe timing failed");
+    }
+    if (rc == HARP_RA_OK &&
+        hipMemcpy(h.data(), clocks, sizeof(long long) * h.size(), hipMemcpyDeviceToHost) != hipSuccess)
+      rc = fail(HARP_RA_ELAUNCH, "probe clock readback failed");
+  }
+  if (rc == HARP_RA_OK) {
+    double shader = 0.0, wall = 0.0;
+    for (int i = 0; i < blocks; ++i) {
+      shader += (double)h[2 * i];
+      wall += (double)h[2 * i + 1];
+    }
+    const double flop = (double)blocks * 4.0 /* waves */ * 4.0 * iters * 32.0 * 32.0 * 16.0 * 2.0;
+    *tflops = (best_ms > 0.f) ? flop / (best_ms * 1e-3) / 1e12 : 0.0;
+    *shader_ghz = (wall > 0.0) ? shader / wall * wall_khz * 1e-6 : 0.0;
+  }
+  if (e0) (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
+  if (sink) (void)hipFree(sink);
+  if (clocks) (void)hipFree(clocks);
+  return rc == HARP_RA_OK ? ok() : rc;
+}
+
 size_t harp_ra_forward_workspace_bytes(int batch, int h_num, int h_len, int sp_size, int kv_chunk_len,
                                        const int32_t* kv_valid_lens) {
   Geometry g;

@@ -305,6 +305,19 @@ __device__ __forceinline__ void pin_agpr(bf16x8& x) { asm volatile("" : "+a"(x))
 __device__ __forceinline__ void settle(bf16x8& x) { asm volatile("" : "+v"(x)); }
 __device__ __forceinline__ void settle(float& x) { asm volatile("" : "+v"(x)); }
 
+// Wave issue priority: a wave raises its priority for its MFMA phases and
+// drops it for softmax / bookkeeping, so when the two waves of a SIMD both
+// have work the one feeding the matrix core issues first.
+#ifndef HARP_SETPRIO
+#define HARP_SETPRIO 1
+#endif
+__device__ __forceinline__ void prio_mfma() {
+  if (HARP_SETPRIO) __builtin_amdgcn_s_setprio(1);
+}
+__device__ __forceinline__ void prio_valu() {
+  if (HARP_SETPRIO) __builtin_amdgcn_s_setprio(0);
+}
+
 // Scheduling fence: the compiler may not move any instruction across it.
 __device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
 
@@ -502,6 +515,7 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
     wait_lds_loads();
     __syncthreads();
     if (nstep < p.ct.n) issue(nstep, nk0, buf ^ 1);
+    prio_mfma();
     // S^T (keys x queries), KB 32-key blocks; step i = (ks = i / KB, kb = i % KB)
     f32x16 s[KB];
 #pragma unroll
@@ -519,6 +533,7 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
           if (kb * 32 + c_row(r, g) >= kv_left) s[kb][r] = -INFINITY;
     }
 
+    prio_valu();
     // online softmax, lane = query
     float mx = -INFINITY;
 #pragma unroll
@@ -551,11 +566,13 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
           pf[kb * 2 + hf][j] = (bf16)e;
         }
 
+    prio_mfma();
     // O^T += V^T P^T; step i = (ks2 = i / DBLK, db = i % DBLK), 16 keys per ks2
     pipelined<2 * KB * DBLK, 2>(
         [&](int i) { return vlo.tr_frag(Vs[buf][(i / DBLK) / 4], ((i / DBLK) % 4) * 16, i % DBLK); },
         [&](int i, const bf16x8& a) { o[i % DBLK] = mfma32x32x16(a, pf[i / DBLK], o[i % DBLK]); });
 
+    prio_valu();
     buf ^= 1;
     step = nstep;
     k0 = nk0;
@@ -763,6 +780,7 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
           [&](int i) { return klo.tr_frag_lean(K, (j & 1) * 32 + (i / DBLK) * 16, i % DBLK); },
           [&](int i, const bf16x8& a) { dq[i % DBLK] = mfma32x32x16(a, dsf[j & 1][i / DBLK], dq[i % DBLK]); });
     };
+    prio_mfma();
     phase_a(Int<0>{}, Int<-1>{});
     phase_a(Int<1>{}, Int<0>{});
     phase_c(Int<0>{});
@@ -772,8 +790,11 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
       phase_a(Int<3>{}, Int<2>{});
       phase_c(Int<2>{});
     }
+    prio_valu();
     softmax_rows(KB - 1, 0, 16);
+    prio_mfma();
     phase_c(Int<KB - 1>{});
+    prio_valu();
 
     buf ^= 1;
     step = nstep;
@@ -930,6 +951,7 @@ __global__ __launch_bounds__(64 * kDkWaves, 1) void dkdv_kernel(BwdParams p) {
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb) {
         const float2 st = stats_lane(buf, qb);
+        prio_mfma();
         f32x16 s = zero16(), dp = zero16();
         pipelined<KSTEPS, 1>(
             [&](int ks) { return Frag2{lo.row_frag_lean(Q, qb, ks), lo.row_frag_lean(Gd, qb, ks)}; },
@@ -938,6 +960,7 @@ __global__ __launch_bounds__(64 * kDkWaves, 1) void dkdv_kernel(BwdParams p) {
               s = mfma32x32x16(f.a, kf[ks], s);
               dp = mfma32x32x16(f.b, v, dp);
             });
+        prio_valu();
         bf16x8 pf[2], dsf[2];
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -945,6 +968,7 @@ __global__ __launch_bounds__(64 * kDkWaves, 1) void dkdv_kernel(BwdParams p) {
           pf[r >> 3][r & 7] = (bf16)pv;
           dsf[r >> 3][r & 7] = (bf16)(pv * (dp[r] - row_bcast(st.y, r)));
         }
+        prio_mfma();
         // dV += P^T dO ; dK += dS^T Q (M = keys, N = d, K = the 32 queries of
         // this half); step s2 = (h2 = s2 / DBLK, db = s2 % DBLK)
         pipelined<2 * DBLK, 1>(
@@ -958,6 +982,7 @@ __global__ __launch_bounds__(64 * kDkWaves, 1) void dkdv_kernel(BwdParams p) {
               dk[db] = mfma32x32x16(dsf[h2], f.b, dk[db]);
             });
       }
+      prio_valu();
       if (t + 1 < n_tiles) store_stats(buf ^ 1);
       buf ^= 1;
     }

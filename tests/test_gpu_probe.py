@@ -1,0 +1,26 @@
+"""GPU test of the sustained-MFMA probe exported by libharp_ra.so (a
+measurement aid with no reference counterpart): it runs, reports a rate
+between a tenth of and the published dense bf16 peak, and a plausible shader
+clock."""
+
+import pytest
+import torch
+
+from harp_amd import _lib
+
+PEAK_BF16_TFLOPS = 2516.6
+
+
+@pytest.mark.gpu
+def test_probe_mfma_rate_is_plausible():
+    torch.cuda.init()
+    tf, ghz = _lib.probe_mfma_rate(1024, 3407)
+    print(f"sustained bf16 MFMA {tf:.1f} TFLOP/s at {ghz:.3f} GHz", flush=True)
+    assert 0.1 * PEAK_BF16_TFLOPS < tf <= 1.02 * PEAK_BF16_TFLOPS
+    assert 0.5 < ghz < 3.0
+
+
+@pytest.mark.gpu
+def test_probe_rejects_bad_arguments():
+    with pytest.raises(RuntimeError, match="iters"):
+        _lib.probe_mfma_rate(3, 1)
