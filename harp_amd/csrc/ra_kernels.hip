@@ -137,15 +137,17 @@ struct DirectLoader {
       voff[k] = ok ? (uint32_t)(r * row_stride * 2 + c * 16) : kOOB;
     }
   }
+  // this wave's k-th copy instruction of the tile (k < kInst)
+  __device__ __forceinline__ void load_one(rsrc_t rs, bf16* tile, int k) const {
+    const int inst = wave + k * NW;
+    if (kInstTot % NW == 0 || inst < kInstTot) {
+      const uint32_t lds = (uint32_t)(uintptr_t)(lds_void*)(tile + inst * 512);
+      lds_dma_b128(rs, __builtin_amdgcn_readfirstlane(lds), voff[k]);
+    }
+  }
   __device__ __forceinline__ void load(rsrc_t rs, bf16* tile) const {
 #pragma unroll
-    for (int k = 0; k < kInst; ++k) {
-      const int inst = wave + k * NW;
-      if (kInstTot % NW == 0 || inst < kInstTot) {
-        const uint32_t lds = (uint32_t)(uintptr_t)(lds_void*)(tile + inst * 512);
-        lds_dma_b128(rs, __builtin_amdgcn_readfirstlane(lds), voff[k]);
-      }
-    }
+    for (int k = 0; k < kInst; ++k) load_one(rs, tile, k);
   }
 };
 
@@ -418,16 +420,34 @@ __device__ __forceinline__ void decode_block(int n_tiles, int H, int& tile, int&
   b = bh / H;
 }
 
-// Next (ring step, first key) after the tile of tile_keys keys at (step, k0),
-// skipping empty chunks.
-__device__ __forceinline__ void next_tile(const ChunkTable& ct, int step, int k0, int tile_keys, int& nstep,
-                                          int& nk0) {
-  nstep = step;
-  nk0 = k0 + tile_keys;
-  while (nstep < ct.n && nk0 >= ct.len[ct.order[nstep]]) {
-    ++nstep;
-    nk0 = 0;
+// Position of a streamed KV tile in the ring: ring step, first key, and the
+// visited chunk's valid length and K / V bases (offset to this (b, h)).  The
+// cursor lives in scalar registers, so moving to the next tile reads the
+// chunk table (kernel arguments: dependent scalar loads of ~200 cycles each)
+// only when it crosses into the next chunk, not on every tile.
+struct KvCursor {
+  int step, k0, len;
+  const bf16* k;
+  const bf16* v;
+};
+// first non-empty chunk from ring step `step` on (step == ct.n: past the end)
+__device__ __forceinline__ void kv_enter(const ChunkTable& ct, int64_t kvo, int step, KvCursor& c) {
+  while (step < ct.n && ct.len[ct.order[step]] == 0) ++step;
+  c.step = step;
+  c.k0 = 0;
+  if (step < ct.n) {
+    const int ch = ct.order[step];
+    c.len = ct.len[ch];
+    c.k = ct.k[ch] + kvo;
+    c.v = ct.v[ch] + kvo;
   }
+}
+// the tile after the one of tile_keys keys at c
+__device__ __forceinline__ KvCursor kv_next(const ChunkTable& ct, int64_t kvo, const KvCursor& c, int tile_keys) {
+  KvCursor n = c;
+  n.k0 = c.k0 + tile_keys;
+  if (n.k0 >= c.len) kv_enter(ct, kvo, c.step + 1, n);
+  return n;
 }
 
 // ---------------------------------------------------------------------------
@@ -492,29 +512,27 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
   float l_run = 0.f;        // this lane-half's partial sum of exp2(s*c2 - m_ref)
 
   const int64_t kvo = (int64_t)b * p.skb + (int64_t)h * p.skh;
-  auto issue = [&](int step, int k0, int bf) {
-    const int c = p.ct.order[step];
+  auto issue = [&](const KvCursor& t, int bf) {
 #pragma unroll
     for (int sb = 0; sb < NS; ++sb) {
-      const int r0 = k0 + 64 * sb, rows = p.ct.len[c] - r0;
-      kld.load(rows_rsrc(p.ct.k[c] + kvo, p.skt, r0, rows), Ks[bf][sb]);
-      vld.load(rows_rsrc(p.ct.v[c] + kvo, p.skt, r0, rows), Vs[bf][sb]);
+      const int r0 = t.k0 + 64 * sb, rows = t.len - r0;
+      kld.load(rows_rsrc(t.k, p.skt, r0, rows), Ks[bf][sb]);
+      vld.load(rows_rsrc(t.v, p.skt, r0, rows), Vs[bf][sb]);
     }
   };
-  int step = 0, k0 = 0;
-  while (step < p.ct.n && p.ct.len[p.ct.order[step]] == 0) ++step;
+  KvCursor cur;
+  kv_enter(p.ct, kvo, 0, cur);
   int buf = 0;
-  if (step < p.ct.n) issue(step, 0, 0);
+  if (cur.step < p.ct.n) issue(cur, 0);
 #pragma unroll
   for (int ks = 0; ks < KSTEPS; ++ks) settle(qf[ks]);
 #pragma unroll 1
-  while (step < p.ct.n) {
-    const int kv_left = p.ct.len[p.ct.order[step]] - k0;
-    int nstep, nk0;
-    next_tile(p.ct, step, k0, 64 * NS, nstep, nk0);
+  while (cur.step < p.ct.n) {
+    const int kv_left = cur.len - cur.k0;
+    const KvCursor nxt = kv_next(p.ct, kvo, cur, 64 * NS);
     wait_lds_loads();
     __syncthreads();
-    if (nstep < p.ct.n) issue(nstep, nk0, buf ^ 1);
+    if (nxt.step < p.ct.n) issue(nxt, buf ^ 1);
     prio_mfma();
     // S^T (keys x queries), KB 32-key blocks; step i = (ks = i / KB, kb = i % KB)
     f32x16 s[KB];
@@ -574,8 +592,7 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
 
     prio_valu();
     buf ^= 1;
-    step = nstep;
-    k0 = nk0;
+    cur = nxt;
   }
 
   // l relative to the exact max: l * 2^(m_ref - m_max)
@@ -712,19 +729,41 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
   for (int i = 0; i < DBLK; ++i) dq[i] = zero16();
 
   const int64_t kvo = (int64_t)b * p.skb + (int64_t)h * p.skh;
-  auto issue = [&](int step, int k0, int bf) {
-    const int c = p.ct.order[step];
+  auto issue = [&](const KvCursor& t, int bf) {
 #pragma unroll
     for (int sb = 0; sb < NS; ++sb) {
-      const int r0 = k0 + 64 * sb, rows = p.ct.len[c] - r0;
-      kld.load(rows_rsrc(p.ct.k[c] + kvo, p.skt, r0, rows), Ks[bf][sb]);
-      vld.load(rows_rsrc(p.ct.v[c] + kvo, p.skt, r0, rows), Vs[bf][sb]);
+      const int r0 = t.k0 + 64 * sb, rows = t.len - r0;
+      kld.load(rows_rsrc(t.k, p.skt, r0, rows), Ks[bf][sb]);
+      vld.load(rows_rsrc(t.v, p.skt, r0, rows), Vs[bf][sb]);
     }
   };
-  int step = 0, k0 = 0;
-  while (step < p.ct.n && p.ct.len[p.ct.order[step]] == 0) ++step;
+  // The next tile's copies are issued one instruction per MFMA step of the
+  // first two S^T / dP^T phases instead of in one burst after the barrier:
+  // a burst of ~80 one-KiB copies per CU keeps the texture unit's FIFOs
+  // full for ~1000 cycles, and a wave stalled on issuing a copy cannot issue
+  // MFMAs either.  Slot j < kDmaSlots: sub-tile j / kSlotsPerSub, K copies
+  // first, then V copies.
+  constexpr int kSlotsK = DirectLoader<GK, kDqWaves>::kInst, kSlotsV = DirectLoader<GV, kDqWaves>::kInst;
+  constexpr int kSlotsPerSub = kSlotsK + kSlotsV, kDmaSlots = NS * kSlotsPerSub;
+  constexpr int kSlotsPerStep = (kDmaSlots + 2 * KSTEPS - 1) / (2 * KSTEPS);
+  rsrc_t nk_rs[NS], nv_rs[NS];
+  auto prepare = [&](const KvCursor& t) {
+#pragma unroll
+    for (int sb = 0; sb < NS; ++sb) {
+      const int r0 = t.k0 + 64 * sb, rows = t.len - r0;
+      nk_rs[sb] = rows_rsrc(t.k, p.skt, r0, rows);
+      nv_rs[sb] = rows_rsrc(t.v, p.skt, r0, rows);
+    }
+  };
+  auto dma_slot = [&](int j, int bf) {
+    const int sb = j / kSlotsPerSub, k = j % kSlotsPerSub;
+    if (k < kSlotsK) kld.load_one(nk_rs[sb], Ks[bf][sb], k);
+    else vld.load_one(nv_rs[sb], Vs[bf][sb], k - kSlotsK);
+  };
+  KvCursor cur;
+  kv_enter(p.ct, kvo, 0, cur);
   int buf = 0;
-  if (step < p.ct.n) issue(step, 0, 0);
+  if (cur.step < p.ct.n) issue(cur, 0);
 #pragma unroll
   for (int ks = 0; ks < KSTEPS; ++ks) {
     settle(qf[ks]);
@@ -734,12 +773,12 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
   settle(lse2_s);
   settle(dlt_s);
 #pragma unroll 1
-  while (step < p.ct.n) {
-    int nstep, nk0;
-    next_tile(p.ct, step, k0, 64 * NS, nstep, nk0);
+  while (cur.step < p.ct.n) {
+    const KvCursor nxt = kv_next(p.ct, kvo, cur, 64 * NS);
     wait_lds_loads();
     __syncthreads();
-    if (nstep < p.ct.n) issue(nstep, nk0, buf ^ 1);
+    const bool has_next = nxt.step < p.ct.n;
+    if (has_next) prepare(nxt);
 
     // S^T / dP^T of two 32-key blocks in flight (block j in slot j & 1) and
     // the bf16 dS^T of the block whose dQ product is next
@@ -765,6 +804,15 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
           [&](int ks) { return Frag2{klo.row_frag_lean(K, j & 1, ks), vlo.frag(V, j & 1, ks)}; },
           [&](int ks, const Frag2& f) {
             s[j & 1] = mfma32x32x16(f.a, qf[ks], s[j & 1]);
+            if constexpr (j < 2) {
+              if (has_next) {
+#pragma unroll
+                for (int u = 0; u < kSlotsPerStep; ++u) {
+                  const int slot = (j * KSTEPS + ks) * kSlotsPerStep + u;
+                  if (slot < kDmaSlots) dma_slot(slot, buf ^ 1);
+                }
+              }
+            }
             dp[j & 1] = mfma32x32x16(f.b, gf[ks], dp[j & 1]);
             if constexpr (jb >= 0) {
               const int r0 = ks * kRowsPerStep;
@@ -797,8 +845,7 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
     prio_valu();
 
     buf ^= 1;
-    step = nstep;
-    k0 = nk0;
+    cur = nxt;
   }
 
   if (!q_ok) return;
