@@ -307,18 +307,27 @@ __device__ __forceinline__ void pin_agpr(bf16x8& x) { asm volatile("" : "+a"(x))
 __device__ __forceinline__ void settle(bf16x8& x) { asm volatile("" : "+v"(x)); }
 __device__ __forceinline__ void settle(float& x) { asm volatile("" : "+v"(x)); }
 
-// Wave issue priority: a wave raises its priority for its MFMA phases and
-// drops it for softmax / bookkeeping, so when the two waves of a SIMD both
-// have work the one feeding the matrix core issues first.
+// Wave issue priority (s_setprio, 0..3) within a tile.  Two waves share a
+// SIMD and the issue arbiter otherwise favours the older one, which then
+// runs a whole phase ahead and idles at the next barrier while its partner
+// finishes alone.  Mode 2 (default): the level falls as a wave moves through
+// the tile, so the wave that lags gets precedence and both reach the barrier
+// together.  Mode 1: level 1 for MFMA phases, 0 for softmax / bookkeeping.
 #ifndef HARP_SETPRIO
 #define HARP_SETPRIO 1
 #endif
-__device__ __forceinline__ void prio_mfma() {
-  if (HARP_SETPRIO) __builtin_amdgcn_s_setprio(1);
+#ifndef HARP_PRIO_MODE
+#define HARP_PRIO_MODE 2
+#endif
+template <int M1, int M2>
+__device__ __forceinline__ void prio_at() {
+  constexpr int lv = HARP_PRIO_MODE == 2 ? M2 : M1;
+  if constexpr (lv >= 0) {
+    if (HARP_SETPRIO) __builtin_amdgcn_s_setprio(lv);
+  }
 }
-__device__ __forceinline__ void prio_valu() {
-  if (HARP_SETPRIO) __builtin_amdgcn_s_setprio(0);
-}
+__device__ __forceinline__ void prio_mfma() { prio_at<1, -1>(); }
+__device__ __forceinline__ void prio_valu() { prio_at<0, -1>(); }
 
 // Scheduling fence: the compiler may not move any instruction across it.
 __device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
@@ -533,7 +542,7 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
     wait_lds_loads();
     __syncthreads();
     if (nxt.step < p.ct.n) issue(nxt, buf ^ 1);
-    prio_mfma();
+    prio_at<1, 3>();
     // S^T (keys x queries), KB 32-key blocks; step i = (ks = i / KB, kb = i % KB)
     f32x16 s[KB];
 #pragma unroll
@@ -551,7 +560,7 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
           if (kb * 32 + c_row(r, g) >= kv_left) s[kb][r] = -INFINITY;
     }
 
-    prio_valu();
+    prio_at<0, 2>();
     // online softmax, lane = query
     float mx = -INFINITY;
 #pragma unroll
@@ -584,13 +593,13 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
           pf[kb * 2 + hf][j] = (bf16)e;
         }
 
-    prio_mfma();
+    prio_at<1, 1>();
     // O^T += V^T P^T; step i = (ks2 = i / DBLK, db = i % DBLK), 16 keys per ks2
     pipelined<2 * KB * DBLK, 2>(
         [&](int i) { return vlo.tr_frag(Vs[buf][(i / DBLK) / 4], ((i / DBLK) % 4) * 16, i % DBLK); },
         [&](int i, const bf16x8& a) { o[i % DBLK] = mfma32x32x16(a, pf[i / DBLK], o[i % DBLK]); });
 
-    prio_valu();
+    prio_at<0, 0>();
     buf ^= 1;
     cur = nxt;
   }
@@ -828,21 +837,23 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
           [&](int i) { return klo.tr_frag_lean(K, (j & 1) * 32 + (i / DBLK) * 16, i % DBLK); },
           [&](int i, const bf16x8& a) { dq[i % DBLK] = mfma32x32x16(a, dsf[j & 1][i / DBLK], dq[i % DBLK]); });
     };
-    prio_mfma();
+    prio_at<1, 3>();
     phase_a(Int<0>{}, Int<-1>{});
     phase_a(Int<1>{}, Int<0>{});
     phase_c(Int<0>{});
     if constexpr (KB > 2) {
+      prio_at<-1, 2>();
       phase_a(Int<2>{}, Int<1>{});
       phase_c(Int<1>{});
+      prio_at<-1, 1>();
       phase_a(Int<3>{}, Int<2>{});
       phase_c(Int<2>{});
     }
-    prio_valu();
+    prio_at<0, 0>();
     softmax_rows(KB - 1, 0, 16);
-    prio_mfma();
+    prio_at<1, 0>();
     phase_c(Int<KB - 1>{});
-    prio_valu();
+    prio_at<0, 0>();
 
     buf ^= 1;
     cur = nxt;
@@ -931,9 +942,7 @@ __global__ __launch_bounds__(64 * kDkWaves, 1) void dkdv_kernel(BwdParams p) {
     // bits when it issues the tile and converts them only in store_stats,
     // after the wait that precedes the barrier.
     uint32_t m_bits = 0, l_bits = 0, d_bits = 0;
-    auto issue = [&](int q0, int bf) {
-      qld.load(rows_rsrc(qb_, p.sqt, q0, p.T - q0), QG[bf][0]);
-      gld.load(rows_rsrc(gb_, p.sdt, q0, p.T - q0), QG[bf][1]);
+    auto issue_stats = [&](int q0) {
       if (tid < 64) {
         const int qq = q0 + tid;
         m_bits = l_bits = d_bits = 0;  // l = 0 marks a row past T: P = 0
@@ -945,6 +954,19 @@ __global__ __launch_bounds__(64 * kDkWaves, 1) void dkdv_kernel(BwdParams p) {
         }
       }
     };
+    auto issue = [&](int q0, int bf) {
+      qld.load(rows_rsrc(qb_, p.sqt, q0, p.T - q0), QG[bf][0]);
+      gld.load(rows_rsrc(gb_, p.sdt, q0, p.T - q0), QG[bf][1]);
+      issue_stats(q0);
+    };
+    // Inside the loop the next tile's copies are issued one instruction per
+    // MFMA step of the first S / dP phase rather than in one burst after
+    // the barrier (a burst fills the texture unit's FIFOs, and a wave
+    // stalled on issuing a copy cannot issue MFMAs); the statistics loads
+    // follow the copies.  Slot j: Q copies, then dO copies.
+    constexpr int kSlotsQ = DirectLoader<GQ, kDkWaves>::kInst, kDmaSlots = 2 * kSlotsQ;
+    constexpr int kSlotsPerStep = (kDmaSlots + KSTEPS - 1) / KSTEPS;
+    rsrc_t nq_rs, ng_rs;
     auto store_stats = [&](int bf) {
       if (tid < 64) {
         const float mm = __uint_as_float(p.m_bf16 ? m_bits << 16 : m_bits);
@@ -992,22 +1014,38 @@ __global__ __launch_bounds__(64 * kDkWaves, 1) void dkdv_kernel(BwdParams p) {
     for (int t = 0; t < n_tiles; ++t) {
       wait_lds_loads();
       __syncthreads();  // tile t published; every wave is done with tile t-1
-      if (t + 1 < n_tiles) issue((t + 1) * 64, buf ^ 1);
+      const bool has_next = t + 1 < n_tiles;
+      const int nq0 = (t + 1) * 64;
+      if (has_next) {
+        nq_rs = rows_rsrc(qb_, p.sqt, nq0, p.T - nq0);
+        ng_rs = rows_rsrc(gb_, p.sdt, nq0, p.T - nq0);
+      }
       const bf16* Q = QG[buf][0];
       const bf16* Gd = QG[buf][1];
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb) {
         const float2 st = stats_lane(buf, qb);
-        prio_mfma();
+        if (qb == 0) prio_at<1, 3>();
+        else prio_at<1, 1>();
         f32x16 s = zero16(), dp = zero16();
         pipelined<KSTEPS, 1>(
             [&](int ks) { return Frag2{lo.row_frag_lean(Q, qb, ks), lo.row_frag_lean(Gd, qb, ks)}; },
             [&](int ks, const Frag2& f) {
               const bf16x8 v = vlo.frag(Vw, vrb, ks);
               s = mfma32x32x16(f.a, kf[ks], s);
+              if (qb == 0 && has_next) {
+#pragma unroll
+                for (int u = 0; u < kSlotsPerStep; ++u) {
+                  const int j = ks * kSlotsPerStep + u;
+                  if (j < kSlotsQ) qld.load_one(nq_rs, QG[buf ^ 1][0], j);
+                  else if (j < kDmaSlots) gld.load_one(ng_rs, QG[buf ^ 1][1], j - kSlotsQ);
+                }
+                if (ks == KSTEPS - 1) issue_stats(nq0);
+              }
               dp = mfma32x32x16(f.b, v, dp);
             });
-        prio_valu();
+        if (qb == 0) prio_at<0, 3>();
+        else prio_at<0, 1>();
         bf16x8 pf[2], dsf[2];
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -1015,7 +1053,8 @@ __global__ __launch_bounds__(64 * kDkWaves, 1) void dkdv_kernel(BwdParams p) {
           pf[r >> 3][r & 7] = (bf16)pv;
           dsf[r >> 3][r & 7] = (bf16)(pv * (dp[r] - row_bcast(st.y, r)));
         }
-        prio_mfma();
+        if (qb == 0) prio_at<1, 2>();
+        else prio_at<1, 0>();
         // dV += P^T dO ; dK += dS^T Q (M = keys, N = d, K = the 32 queries of
         // this half); step s2 = (h2 = s2 / DBLK, db = s2 % DBLK)
         pipelined<2 * DBLK, 1>(
@@ -1029,7 +1068,7 @@ __global__ __launch_bounds__(64 * kDkWaves, 1) void dkdv_kernel(BwdParams p) {
               dk[db] = mfma32x32x16(dsf[h2], f.b, dk[db]);
             });
       }
-      prio_valu();
+      prio_at<0, 0>();
       if (t + 1 < n_tiles) store_stats(buf ^ 1);
       buf ^= 1;
     }
