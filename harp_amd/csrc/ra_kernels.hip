@@ -529,6 +529,21 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
       vld.load(rows_rsrc(t.v, p.skt, r0, rows), Vs[bf][sb]);
     }
   };
+  // Inside the loop the next tile's copies are issued spread over the S^T
+  // MFMA steps (slot j at step j * kSlotStride) rather than in one burst
+  // after the barrier: a burst fills the texture unit's FIFOs, and a wave
+  // stalled on issuing a copy cannot issue MFMAs.  Slot j: sub-tile
+  // j / kSlotsPerSub, K copies first, then V copies.
+  constexpr int kSlotsK = DirectLoader<GK, kFwdWaves>::kInst, kSlotsV = DirectLoader<GV, kFwdWaves>::kInst;
+  constexpr int kSlotsPerSub = kSlotsK + kSlotsV, kDmaSlots = NS * kSlotsPerSub;
+  constexpr int kSSteps = KB * KSTEPS, kSlotStride = kSSteps / kDmaSlots > 0 ? kSSteps / kDmaSlots : 1;
+  constexpr int kSlotsPerStep = (kDmaSlots + kSSteps - 1) / kSSteps;
+  rsrc_t nk_rs[NS], nv_rs[NS];
+  auto dma_slot = [&](int j, int bf) {
+    const int sb = j / kSlotsPerSub, k = j % kSlotsPerSub;
+    if (k < kSlotsK) kld.load_one(nk_rs[sb], Ks[bf][sb], k);
+    else vld.load_one(nv_rs[sb], Vs[bf][sb], k - kSlotsK);
+  };
   KvCursor cur;
   kv_enter(p.ct, kvo, 0, cur);
   int buf = 0;
@@ -541,14 +556,31 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
     const KvCursor nxt = kv_next(p.ct, kvo, cur, 64 * NS);
     wait_lds_loads();
     __syncthreads();
-    if (nxt.step < p.ct.n) issue(nxt, buf ^ 1);
+    const bool has_next = nxt.step < p.ct.n;
+    if (has_next) {
+#pragma unroll
+      for (int sb = 0; sb < NS; ++sb) {
+        const int r0 = nxt.k0 + 64 * sb, rows = nxt.len - r0;
+        nk_rs[sb] = rows_rsrc(nxt.k, p.skt, r0, rows);
+        nv_rs[sb] = rows_rsrc(nxt.v, p.skt, r0, rows);
+      }
+    }
     prio_at<1, 3>();
     // S^T (keys x queries), KB 32-key blocks; step i = (ks = i / KB, kb = i % KB)
     f32x16 s[KB];
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) s[kb] = zero16();
     pipelined<KB * KSTEPS, 2>([&](int i) { return klo.frag(Ks[buf][(i % KB) / 2], i & 1, i / KB); },
-                              [&](int i, const bf16x8& a) { s[i % KB] = mfma32x32x16(a, qf[i / KB], s[i % KB]); });
+                              [&](int i, const bf16x8& a) {
+                                s[i % KB] = mfma32x32x16(a, qf[i / KB], s[i % KB]);
+                                if (has_next && i % kSlotStride == 0) {
+#pragma unroll
+                                  for (int u = 0; u < kSlotsPerStep; ++u) {
+                                    const int j = (i / kSlotStride) * kSlotsPerStep + u;
+                                    if (j < kDmaSlots) dma_slot(j, buf ^ 1);
+                                  }
+                                }
+                              });
     if (kv_left < 64 * NS) {  // tail tile of a chunk: mask keys past its valid length
       // a side-effecting (empty) asm keeps this a real uniform branch instead
       // of selects that would run on every tile
