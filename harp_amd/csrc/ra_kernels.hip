@@ -479,7 +479,7 @@ constexpr int kFwdSub = HARP_FWD_SUB;
 template <int KSTEPS, int DBLK>
 __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
   constexpr int DP = DBLK * 32;
-  using GK = PadTile<DP>;  // K: row fragments only
+  using GK = XorTile<DP>;  // K: row fragments only
   using GV = XorTile<DP>;  // V: transposed fragments
   constexpr float kTau = 8.f;  // lazy-rescale threshold (log2 units): P <= 2^8
   constexpr int NS = kFwdSub, KB = 2 * NS;  // 64-row sub-tiles, 32-key blocks per tile
@@ -504,8 +504,8 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
       qf[ks] = (q_ok && d0 < p.D) ? *(const bf16x8*)(qrow + d0) : zero8();
     }
   }
-  PadRows<DP> klo;
-  klo.init(lane);
+  XorLanes<DP, KSTEPS> klo;
+  klo.init_rows_lean(lane);
   XorLanes<DP, KSTEPS> vlo;
   vlo.init(lane, false);
   DirectLoader<GK, kFwdWaves> kld;
@@ -570,7 +570,7 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
     f32x16 s[KB];
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) s[kb] = zero16();
-    pipelined<KB * KSTEPS, 2>([&](int i) { return klo.frag(Ks[buf][(i % KB) / 2], i & 1, i / KB); },
+    pipelined<KB * KSTEPS, 2>([&](int i) { return klo.row_frag_lean(Ks[buf][(i % KB) / 2], i & 1, i / KB); },
                               [&](int i, const bf16x8& a) {
                                 s[i % KB] = mfma32x32x16(a, qf[i / KB], s[i % KB]);
                                 if (has_next && i % kSlotStride == 0) {
@@ -726,7 +726,7 @@ template <int KSTEPS, int DBLK>
 __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
   constexpr int DP = DBLK * 32;
   using GK = XorTile<DP>;  // K: row and transposed fragments
-  using GV = PadTile<DP>;  // V: row fragments only
+  using GV = XorTile<DP>;  // V: row fragments only
   constexpr int NS = kDqSub, KB = 2 * NS;
   __shared__ __attribute__((aligned(16))) bf16 Ks[2][NS][GK::ELEMS];
   __shared__ __attribute__((aligned(16))) bf16 Vs[2][NS][GV::ELEMS];
@@ -758,8 +758,8 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
   XorLanes<DP, KSTEPS> klo;
   klo.init_rows_lean(lane);
   klo.init_tr_lean(lane);
-  PadRows<DP> vlo;
-  vlo.init(lane);
+  XorLanes<DP, KSTEPS> vlo;
+  vlo.init_rows_lean(lane);
   DirectLoader<GK, kDqWaves> kld;
   kld.init(p.skt, p.D, wave, lane);
   DirectLoader<GV, kDqWaves> vld;
@@ -842,7 +842,7 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
       dp[j & 1] = zero16();
       constexpr int kRowsPerStep = (16 + KSTEPS - 1) / KSTEPS;
       pipelined<KSTEPS, kDqPfA>(
-          [&](int ks) { return Frag2{klo.row_frag_lean(K, j & 1, ks), vlo.frag(V, j & 1, ks)}; },
+          [&](int ks) { return Frag2{klo.row_frag_lean(K, j & 1, ks), vlo.row_frag_lean(V, j & 1, ks)}; },
           [&](int ks, const Frag2& f) {
             s[j & 1] = mfma32x32x16(f.a, qf[ks], s[j & 1]);
             if constexpr (j < 2) {
