@@ -20,6 +20,7 @@ ROOT = Path(__file__).resolve().parent.parent
 KERNELS = ROOT / "kernels"
 ABI_LIB = KERNELS / "libharp_ra.so"
 OPS_LIB = KERNELS / "libring_attention_ops.so"
+ASYNC_OPS_LIB = KERNELS / "libharp_async_op.so"
 
 HARP_RA_OK = 0
 HARP_RA_EINVAL = 1
@@ -34,6 +35,7 @@ KERNEL_KINDS = ("pack", "fwd", "delta", "dkdv", "dq")
 _lock = threading.Lock()
 _abi: ctypes.CDLL | None = None
 _ops_loaded = False
+_async_ops_loaded = False
 
 _p = ctypes.c_void_p
 _i = ctypes.c_int
@@ -67,6 +69,26 @@ ABI_PROTOTYPES = {
 }
 
 
+HARP_QK_OK = 0
+HARP_QK_F32 = 0
+HARP_QK_BF16 = 1
+_f = ctypes.c_float
+_i64 = ctypes.c_int64
+# (restype, argtypes) of every symbol include/harp_qk_norm_rope.h declares
+QK_PROTOTYPES = {
+    "harp_qk_rmsnorm_forward": (_i, [_p, _i64p, _p, _i64p, _p, _i, _p, _f, _i, _i, _i, _i, _p]),
+    "harp_qk_rmsnorm_backward": (_i, [_p, _i64p, _p, _i64p, _p, _i, _p, _p, _i64p, _p, _i, _i, _i, _i, _i,
+                                      _p, _sz, _p]),
+    "harp_qk_rope_forward": (_i, [_p, _i64p, _p, _i64, _i64, _p, _i64p, _i, _i, _i, _i, _p]),
+    "harp_qk_rope_backward": (_i, [_p, _i64p, _p, _i64, _i64, _p, _i64p, _i, _i, _i, _i, _p]),
+    "harp_qk_norm_rope_forward": (_i, [_p, _i64p, _p, _i, _f, _p, _i64, _i64, _p, _i64p, _p, _i, _i, _i, _i, _p]),
+    "harp_qk_norm_rope_backward": (_i, [_p, _i64p, _p, _i64p, _p, _i, _p, _p, _i64, _i64, _p, _i64p, _p, _i,
+                                        _i, _i, _i, _i, _p, _sz, _p]),
+    "harp_qk_backward_workspace_bytes": (_sz, [_i, _i, _i, _i]),
+    "harp_qk_last_error": (ctypes.c_char_p, []),
+}
+
+
 def _missing(path: Path) -> RuntimeError:
     return RuntimeError(
         f"{path} is not built; run `python -m harp_amd.build` (or __graft_entry__.build()). "
@@ -82,7 +104,7 @@ def load_abi() -> ctypes.CDLL:
             if not ABI_LIB.exists():
                 raise _missing(ABI_LIB)
             lib = ctypes.CDLL(str(ABI_LIB))
-            for name, (res, args) in ABI_PROTOTYPES.items():
+            for name, (res, args) in {**ABI_PROTOTYPES, **QK_PROTOTYPES}.items():
                 fn = getattr(lib, name)
                 fn.restype = res
                 fn.argtypes = args
@@ -100,6 +122,23 @@ def load_ops() -> None:
             raise _missing(OPS_LIB)
         torch.ops.load_library(str(OPS_LIB))
         _ops_loaded = True
+
+
+def load_async_ops() -> None:
+    """Register torch.ops.async_op (QK RMSNorm, RoPE) from kernels/libharp_async_op.so."""
+    global _async_ops_loaded
+    with _lock:
+        if _async_ops_loaded:
+            return
+        if not ASYNC_OPS_LIB.exists():
+            raise _missing(ASYNC_OPS_LIB)
+        torch.ops.load_library(str(ASYNC_OPS_LIB))
+        _async_ops_loaded = True
+
+
+def qk_check(rc: int, what: str) -> None:
+    if rc != HARP_QK_OK:
+        raise RuntimeError(f"{what} failed (status {rc}): {load_abi().harp_qk_last_error().decode()}")
 
 
 def last_error() -> str:

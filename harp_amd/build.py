@@ -1,14 +1,18 @@
 """Build the gfx950 libraries in-tree (no JIT cache, no setuptools).
 
-Outputs (both under ``kernels/`` at the repository root, next to each other
-so the operator library finds the C-ABI library through ``$ORIGIN``):
+Outputs (all under ``kernels/`` at the repository root, next to each other
+so the operator libraries find the C-ABI library through ``$ORIGIN``):
 
-* ``libharp_ra.so``              HIP kernels + the C ABI of include/harp_ring_attn.h
+* ``libharp_ra.so``              HIP kernels + the C ABIs of include/harp_ring_attn.h
+                                 and include/harp_qk_norm_rope.h
                                  (hipcc, --offload-arch=gfx950).
 * ``libring_attention_ops.so``   the PyTorch operator library (namespace
                                  ``ring_attention_ops``), the drop-in for the
                                  reference's kernels/libring_attention_ops.so
                                  (gemm/ring_attention/Makefile:9-12, 36-37).
+* ``libharp_async_op.so``        the PyTorch operator library for the QK RMSNorm
+                                 and RoPE operators (namespace ``async_op``,
+                                 async_rt/csrc/async_op_api.cc:54-57), on the GPU.
 
 Run ``python -m harp_amd.build`` (or ``__graft_entry__.build()``).
 """
@@ -26,10 +30,12 @@ INCLUDE = ROOT / "include"
 OUT = ROOT / "kernels"
 ABI_LIB = OUT / "libharp_ra.so"
 OPS_LIB = OUT / "libring_attention_ops.so"
+ASYNC_OPS_LIB = OUT / "libharp_async_op.so"
 
-HIP_SOURCES = ["ra_kernels.hip", "ra_abi.hip", "ra_probe.hip"]
-HIP_HEADERS = ["ra_common.h", "ra_kernels.h"]
+HIP_SOURCES = ["ra_kernels.hip", "ra_abi.hip", "ra_probe.hip", "qk_kernels.hip", "qk_abi.hip"]
+HIP_HEADERS = ["ra_common.h", "ra_kernels.h", "qk_kernels.h"]
 OPS_SOURCE = "torch_ring_attention_ops.cpp"
+ASYNC_OPS_SOURCE = "torch_async_op.cpp"
 
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 OFFLOAD_ARCH = "gfx950"
@@ -74,13 +80,14 @@ def build_abi(verbose: bool = False) -> Path:
     return ABI_LIB
 
 
-def build_ops(verbose: bool = False) -> Path:
+def build_ops(verbose: bool = False, source: str = OPS_SOURCE, lib: Path = OPS_LIB,
+              ext_name: str = "ring_attention_ops") -> Path:
     import torch.utils.cpp_extension as ce
 
     OUT.mkdir(parents=True, exist_ok=True)
     torch_lib = Path(ce.library_paths()[0])
     incs = ce.include_paths()
-    tmp = OPS_LIB.with_suffix(".so.tmp")
+    tmp = lib.with_suffix(".so.tmp")
     abi = int(__import__("torch")._C._GLIBCXX_USE_CXX11_ABI)
     cmd = [
         "g++",
@@ -91,11 +98,11 @@ def build_ops(verbose: bool = False) -> Path:
         "-D__HIP_PLATFORM_AMD__=1",
         "-DUSE_ROCM=1",
         f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
-        "-DTORCH_EXTENSION_NAME=ring_attention_ops",
+        f"-DTORCH_EXTENSION_NAME={ext_name}",
         *[f"-I{p}" for p in incs],
         f"-I{ROCM / 'include'}",
         f"-I{INCLUDE}",
-        str(CSRC / OPS_SOURCE),
+        str(CSRC / source),
         f"-L{OUT}",
         "-lharp_ra",
         f"-L{torch_lib}",
@@ -109,23 +116,30 @@ def build_ops(verbose: bool = False) -> Path:
         str(tmp),
     ]
     _run(cmd, verbose)
-    os.replace(tmp, OPS_LIB)
-    return OPS_LIB
+    os.replace(tmp, lib)
+    return lib
+
+
+def build_async_ops(verbose: bool = False) -> Path:
+    """kernels/libharp_async_op.so: the async_op operators (QK RMSNorm, RoPE)."""
+    return build_ops(verbose, ASYNC_OPS_SOURCE, ASYNC_OPS_LIB, "harp_async_op")
 
 
 def build(verbose: bool = False) -> None:
-    """Compile both libraries unconditionally (the build check)."""
+    """Compile every library unconditionally (the build check)."""
     build_abi(verbose)
     build_ops(verbose)
+    build_async_ops(verbose)
 
 
 def sources_newer_than_libs() -> bool:
     """True when a source file is newer than a built library (or one is missing)."""
-    libs = [ABI_LIB, OPS_LIB]
+    libs = [ABI_LIB, OPS_LIB, ASYNC_OPS_LIB]
     if not all(p.exists() for p in libs):
         return True
     newest_lib = min(p.stat().st_mtime for p in libs)
-    srcs = [CSRC / s for s in HIP_SOURCES + HIP_HEADERS + [OPS_SOURCE]] + [INCLUDE / "harp_ring_attn.h"]
+    srcs = [CSRC / s for s in HIP_SOURCES + HIP_HEADERS + [OPS_SOURCE, ASYNC_OPS_SOURCE]]
+    srcs += [INCLUDE / "harp_ring_attn.h", INCLUDE / "harp_qk_norm_rope.h"]
     return any(s.stat().st_mtime > newest_lib for s in srcs)
 
 

@@ -1,0 +1,139 @@
+/*
+ * harp_qk_norm_rope.h — C ABI of the MI355X (gfx950) kernels for the step
+ * before the ring-attention block: per-head RMSNorm of Q and K and the rotary
+ * embedding (RoPE), forward and backward, separately and fused.
+ *
+ * In HARP these run on the CPU as async_op operators (ARM SVE): the model
+ * applies norm_q / norm_k and then RoPE to the head-split projections
+ * (src/models/z_image/module/attn.py:74-89).  libharp_ra.so exports the
+ * functions declared here next to those of harp_ring_attn.h.
+ *
+ * Conventions (as harp_ring_attn.h): plain device pointers, element strides
+ * {b, h, s, d} of [B, H, S, D] views with d == 1, asynchronous on the given
+ * HIP stream (NULL = default stream), int status (HARP_QK_OK = 0) and
+ * harp_qk_last_error() for the message.  bf16 rows are read and written with
+ * 16-byte accesses: bf16 bases 16-byte aligned, b/h/s strides multiples of 8
+ * elements, D a multiple of 8 (and even, for RoPE), 8 <= D <= 256.
+ *
+ * freqs is the RoPE table as fp32 (cos, sin) pairs: torch.view_as_real of
+ * the complex [S, D/2] (or [B, S, D/2]) freqs_cis, flattened to [.., S, D];
+ * f_stride_b (0 = shared by every batch) and f_stride_s are float strides,
+ * multiples of 4, and the base is 16-byte aligned.
+ *
+ * Numerics follow the reference kernels: fp32 arithmetic, every bf16 result
+ * truncated to its high 16 bits (async_rt/csrc/async_op_math.h:24-35),
+ * rms = sqrt(sum(x^2)/D + eps) kept in fp32.
+ */
+#ifndef HARP_QK_NORM_ROPE_H
+#define HARP_QK_NORM_ROPE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifndef HARP_QK_API
+#define HARP_QK_API __attribute__((visibility("default")))
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  HARP_QK_OK = 0,
+  HARP_QK_EINVAL = 1,       /* bad pointer, size, stride, alignment or dtype */
+  HARP_QK_EUNSUPPORTED = 2, /* valid request this build does not handle (e.g. D > 256) */
+  HARP_QK_ENOMEM = 3,       /* workspace too small / allocation failed */
+  HARP_QK_ELAUNCH = 4       /* HIP launch or runtime error */
+};
+
+enum { HARP_QK_F32 = 0, HARP_QK_BF16 = 1 };
+
+/*
+ * RMSNorm forward: out = (x / rms) * weight, rms = sqrt(mean(x^2) + eps) per
+ * row, written to rms[(b*H + h)*S + s] (fp32) when rms is not NULL.  weight is
+ * [D] (bf16 or fp32 per weight_dtype) or NULL.
+ * Replaces: rmsnorm_forward_out(Tensor input, Tensor weight, Tensor(a!) output,
+ *   Tensor(b!) rms, float eps) — async_rt/csrc/rms_norm.cc:447-482 (kernel
+ *   :20-105), schema async_rt/csrc/async_op_api.cc:54.
+ */
+HARP_QK_API int harp_qk_rmsnorm_forward(const void* x, const int64_t* x_strides, void* out,
+                                        const int64_t* out_strides, const void* weight, int weight_dtype,
+                                        float* rms, float eps, int batch, int h_num, int s_len, int h_len,
+                                        void* stream);
+
+/*
+ * RMSNorm backward: dx from dy, the forward input x and the saved rms;
+ * grad_weight (bf16 or fp32 per grad_weight_dtype, may be NULL) = sum over
+ * all rows of dy * x / rms.  workspace: harp_qk_backward_workspace_bytes()
+ * bytes of device memory, or NULL for a library-owned one.
+ * Replaces: rmsnorm_backward_out(Tensor input, Tensor grad_output, Tensor
+ *   weight, Tensor rms, Tensor(a!) grad_input, Tensor(b!) grad_weight) —
+ *   async_rt/csrc/rms_norm.cc:484-522 (kernel :107-240), schema
+ *   async_op_api.cc:55.  The reference binding passes a NULL weight-gradient
+ *   pointer to its kernel (rms_norm.cc:500-512) and so returns zeros; this
+ *   entry point computes the sum the kernel accumulates (rms_norm.cc:222-229).
+ */
+HARP_QK_API int harp_qk_rmsnorm_backward(const void* x, const int64_t* x_strides, const void* dy,
+                                         const int64_t* dy_strides, const void* weight, int weight_dtype,
+                                         const float* rms, void* dx, const int64_t* dx_strides, void* grad_weight,
+                                         int grad_weight_dtype, int batch, int h_num, int s_len, int h_len,
+                                         void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * RoPE forward: pairs (x[2i], x[2i+1]) times (cos, sin) of row s as complex
+ * numbers.
+ * Replaces: rope_forward_impl(Tensor x, Tensor freqs_cis, Tensor(a!) output) —
+ *   async_rt/csrc/rope.cc:186-215 (kernel :9-86), schema async_op_api.cc:56.
+ */
+HARP_QK_API int harp_qk_rope_forward(const void* x, const int64_t* x_strides, const float* freqs, int64_t f_stride_b,
+                                     int64_t f_stride_s, void* out, const int64_t* out_strides, int batch, int h_num,
+                                     int s_len, int h_len, void* stream);
+
+/*
+ * RoPE backward: the same pairs times the conjugate.
+ * Replaces: rope_backward_impl(Tensor grad_output, Tensor freqs_cis, Tensor(b!)
+ *   grad_x) — async_rt/csrc/rope.cc:217-249 (kernel :88-183), schema
+ *   async_op_api.cc:57.
+ */
+HARP_QK_API int harp_qk_rope_backward(const void* dy, const int64_t* dy_strides, const float* freqs,
+                                      int64_t f_stride_b, int64_t f_stride_s, void* dx, const int64_t* dx_strides,
+                                      int batch, int h_num, int s_len, int h_len, void* stream);
+
+/*
+ * Fused RMSNorm then RoPE in one pass over the rows (read x once, write out
+ * once), the intermediate truncated to bf16 exactly as between the two
+ * reference operators; rms as harp_qk_rmsnorm_forward.  No reference
+ * counterpart as one operator: it replaces the pair norm_q/norm_k ->
+ * ApplyRotaryComplexFn of src/models/z_image/module/attn.py:78-89.
+ */
+HARP_QK_API int harp_qk_norm_rope_forward(const void* x, const int64_t* x_strides, const void* weight,
+                                          int weight_dtype, float eps, const float* freqs, int64_t f_stride_b,
+                                          int64_t f_stride_s, void* out, const int64_t* out_strides, float* rms,
+                                          int batch, int h_num, int s_len, int h_len, void* stream);
+
+/*
+ * Fused backward: RoPE backward of dy (truncated to bf16, as the reference's
+ * intermediate gradient), then RMSNorm backward against x and rms.  No
+ * reference counterpart as one operator (the reverse of the pair above).
+ */
+HARP_QK_API int harp_qk_norm_rope_backward(const void* dy, const int64_t* dy_strides, const void* x,
+                                           const int64_t* x_strides, const void* weight, int weight_dtype,
+                                           const float* rms, const float* freqs, int64_t f_stride_b,
+                                           int64_t f_stride_s, void* dx, const int64_t* dx_strides,
+                                           void* grad_weight, int grad_weight_dtype, int batch, int h_num,
+                                           int s_len, int h_len, void* workspace, size_t workspace_bytes,
+                                           void* stream);
+
+/* Device workspace the two backward entry points with RMSNorm need
+ * ((size_t)-1 when the arguments are invalid): the weight-gradient partial
+ * sums, at most 2048 x h_len floats. */
+HARP_QK_API size_t harp_qk_backward_workspace_bytes(int batch, int h_num, int s_len, int h_len);
+
+/* Last error message of the calling thread ("" if none). */
+HARP_QK_API const char* harp_qk_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HARP_QK_NORM_ROPE_H */

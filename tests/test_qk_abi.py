@@ -1,0 +1,110 @@
+"""CPU tests of the QK-RMSNorm / RoPE boundary: libharp_ra.so exports exactly
+the functions include/harp_qk_norm_rope.h declares, validates arguments on the
+host before touching a device, sizes its workspace, and the async_op operator
+library registers the reference's schemas (no GPU needed)."""
+
+import os
+import re
+import subprocess
+
+import pytest
+import torch
+
+import harp_amd
+from harp_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "harp_qk_norm_rope.h")
+
+# async_rt/csrc/async_op_api.cc:54-57
+REF_SCHEMAS = {
+    "rmsnorm_forward_out": "rmsnorm_forward_out(Tensor input, Tensor weight, Tensor(a!) output, Tensor(b!) rms, "
+                           "float eps) -> ()",
+    "rmsnorm_backward_out": "rmsnorm_backward_out(Tensor input, Tensor grad_output, Tensor weight, Tensor rms, "
+                            "Tensor(a!) grad_input, Tensor(b!) grad_weight) -> ()",
+    "rope_forward_impl": "rope_forward_impl(Tensor x, Tensor freqs_cis, Tensor(a!) output) -> ()",
+    "rope_backward_impl": "rope_backward_impl(Tensor grad_output, Tensor freqs_cis, Tensor(b!) grad_x) -> ()",
+}
+
+
+def header_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"HARP_QK_API\s+[\w\s\*]+?\b(harp_qk_\w+)\s*\(", text)))
+
+
+def test_header_and_prototypes_agree():
+    fns = header_functions()
+    assert len(fns) == 8
+    assert set(fns) == set(_lib.QK_PROTOTYPES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = harp_amd.load_abi()
+    for name in header_functions():
+        assert hasattr(lib, name), name
+    nm = subprocess.run(["nm", "-D", "--defined-only", str(_lib.ABI_LIB)], capture_output=True, text=True)
+    exported = {ln.split()[-1] for ln in nm.stdout.splitlines() if " T " in ln}
+    assert {s for s in exported if s.startswith("harp_qk_")} == set(header_functions())
+
+
+def _strides(b, h, s, d=1):
+    return _lib.i64_array([b, h, s, d])
+
+
+FAKE = 1 << 20  # 16-byte aligned, never dereferenced: validation fails first
+
+
+def _fwd(**over):
+    lib = harp_amd.load_abi()
+    st = _strides(8 * 64 * 128, 64, 8 * 64)
+    a = dict(x=FAKE, xs=st, w=None, wdt=_lib.HARP_QK_BF16, eps=1e-6, f=FAKE, fsb=0, fss=128, out=FAKE, os=st,
+             rms=FAKE, B=1, H=8, S=64, D=128)
+    a.update(over)
+    return lib.harp_qk_norm_rope_forward(a["x"], a["xs"], a["w"], a["wdt"], a["eps"], a["f"], a["fsb"], a["fss"],
+                                         a["out"], a["os"], a["rms"], a["B"], a["H"], a["S"], a["D"], None)
+
+
+@pytest.mark.parametrize("over,msg", [
+    (dict(x=None), "x is NULL"),
+    (dict(x=FAKE + 2), "16-byte aligned"),
+    (dict(D=100), "multiple of 8"),
+    (dict(D=264), "not supported"),
+    (dict(S=0), "positive"),
+    (dict(xs=_strides(8 * 64 * 128, 64, 8 * 64, 2)), "unit stride"),
+    (dict(os=_strides(8 * 64 * 128, 64, 7)), "multiple of 8"),
+    (dict(f=None), "freqs is NULL"),
+    (dict(fss=130), "multiples of 4"),
+    (dict(eps=-1.0), "eps"),
+    (dict(w=FAKE, wdt=7), "dtype"),
+])
+def test_forward_rejects_bad_arguments_on_the_host(over, msg):
+    rc = _fwd(**over)
+    assert rc != _lib.HARP_QK_OK
+    assert msg in harp_amd.load_abi().harp_qk_last_error().decode()
+
+
+def test_backward_validation_and_workspace_size():
+    lib = harp_amd.load_abi()
+    st = _strides(8 * 64 * 128, 64, 8 * 64)
+    rc = lib.harp_qk_rmsnorm_backward(FAKE, st, FAKE, st, None, 1, None, FAKE, st, None, 1, 1, 8, 64, 128,
+                                      None, 0, None)
+    assert rc == 1 and "rms is NULL" in lib.harp_qk_last_error().decode()
+    # 1*8*64 rows -> 32 blocks of 16 rows, 128 floats each
+    assert lib.harp_qk_backward_workspace_bytes(1, 8, 64, 128) == 32 * 128 * 4
+    # capped at 2048 blocks
+    assert lib.harp_qk_backward_workspace_bytes(1, 24, 8192, 128) == 2048 * 128 * 4
+    assert lib.harp_qk_backward_workspace_bytes(1, 8, 64, 100) == 2 ** 64 - 1
+
+
+def test_async_op_schemas_are_the_references():
+    harp_amd.load_async_ops()
+    for name, schema in REF_SCHEMAS.items():
+        got = str(getattr(torch.ops.async_op, name).default._schema)
+        assert got == "async_op::" + schema, got
+
+
+def test_cpu_tensors_are_refused():
+    harp_amd.load_async_ops()
+    x = torch.zeros(1, 2, 3, 64, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="HIP device only"):
+        torch.ops.async_op.rope_forward_impl(x, torch.zeros(3, 32, dtype=torch.complex64), x)
