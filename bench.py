@@ -129,6 +129,89 @@ def cpu_baseline(cfg, target_s: float):
     }
 
 
+def producer_bench(cfg, seed: int, iters: int = 20):
+    """The step before the path: fused QK RMSNorm + RoPE
+    forward and backward (torch.ops.async_op.qk_norm_rope_{forward,backward})
+    on one Q-shaped tensor of the workload ([B, H, T, D] token-major view),
+    timed with HIP events on the current stream.  HBM-bound: algorithmic
+    bytes per call are x in + out (bf16) + rms (fp32) + the RoPE table once per
+    token (forward); dy + x in + dx out (bf16) + rms + table + the
+    weight-gradient partials written and read (backward)."""
+    import torch
+
+    import harp_amd
+    from harp_amd import _lib
+
+    harp_amd.load_async_ops()
+    ops = torch.ops.async_op
+    dev = torch.device("cuda:0")
+    B, H, T, D = cfg["B"], cfg["H"], cfg["T"], cfg["D"]
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn((B, T, H, D), generator=g).to(torch.bfloat16).to(dev).transpose(1, 2)
+    dy = torch.randn((B, T, H, D), generator=g).to(torch.bfloat16).to(dev).transpose(1, 2)
+    w = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16).to(dev)
+    ang = torch.arange(T, dtype=torch.float64)[:, None] * (10000.0 ** (-2.0 * torch.arange(D // 2) / D))[None, :]
+    freqs = torch.polar(torch.ones_like(ang), ang).to(torch.complex64).to(dev)
+    y = torch.empty_like(x)
+    dx = torch.empty_like(x)
+    rms = torch.empty(B * H * T, device=dev, dtype=torch.float32)
+    gw = torch.empty(D, device=dev, dtype=torch.bfloat16)
+    rows = B * H * T
+    ws_bytes = _lib.load_abi().harp_qk_backward_workspace_bytes(B, H, T, D)
+    fwd_bytes = rows * D * 2 * 2 + rows * 4 + T * D * 4
+    bwd_bytes = rows * D * 2 * 3 + rows * 4 + T * D * 4 + 2 * ws_bytes
+    res = {}
+    for name, fn, nbytes in (
+        ("forward", lambda: ops.qk_norm_rope_forward(x, w, freqs, y, rms, 1e-6), fwd_bytes),
+        ("backward", lambda: ops.qk_norm_rope_backward(x, dy, w, rms, freqs, dx, gw), bwd_bytes),
+    ):
+        for _ in range(3):
+            fn()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        torch.cuda.synchronize()
+        ev[0].record()
+        for _ in range(iters):
+            fn()
+        ev[1].record()
+        torch.cuda.synchronize()
+        us = ev[0].elapsed_time(ev[1]) * 1e3 / iters
+        gbs = nbytes / (us * 1e-6) / 1e9
+        res[name] = {"avg_us": round(us, 2), "bytes": int(nbytes), "GB_s": round(gbs, 1),
+                     "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
+    res["shape"] = f"[B,H,T,D]=[{B},{H},{T},{D}] token-major bf16, weight bf16 [D], freqs complex64 [T, D/2]"
+    res["ops"] = "async_op.qk_norm_rope_forward / qk_norm_rope_backward (one of Q, K)"
+    return res
+
+
+def producer_cpu_baseline(cfg, seed: int, target_s: float = 4.0):
+    """The reference's producer math as a CPU restatement (oracle, numpy) on
+    a bounded sample of Q rows: fused forward + backward per row, rows/s."""
+    import numpy as np
+
+    from oracle import qk_norm_rope_oracle as qo
+
+    D, T = cfg["D"], cfg["T"]
+    rng = np.random.default_rng(seed)
+    f = qo.rope_table(T, D)
+    w = qo.f32_to_bf16_rne((1 + 0.1 * rng.standard_normal(D)).astype(np.float32))
+
+    def run(rows):
+        s_len = min(rows, T)
+        x = qo.f32_to_bf16_rne(rng.standard_normal((rows // s_len, s_len, D)).astype(np.float32))
+        dy = qo.f32_to_bf16_rne(rng.standard_normal((rows // s_len, s_len, D)).astype(np.float32))
+        t0 = time.perf_counter()
+        y, rms = qo.norm_rope_forward(x, w, 1e-6, f[:s_len])
+        qo.norm_rope_backward(x, dy, w, rms, f[:s_len])
+        return time.perf_counter() - t0
+
+    run(1024)
+    probe = run(8192)
+    rows = int(max(8192, min(cfg["B"] * cfg["H"] * T, 8192 * target_s / max(probe, 1e-3))) // 8192 * 8192)
+    dt = run(rows)
+    return {"rows_per_s": round(rows / dt, 1), "cores": 1, "kind": "port",
+            "sample": f"{rows} rows of D={D} (fused forward + backward, numpy), {dt:.1f} s on {cpu_model()}"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -138,6 +221,8 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=3407)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU-baseline sample time")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-producer", action="store_true",
+                    help="skip the QK RMSNorm + RoPE (producer step) measurement")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="before the timed steps, run one plain device copy of this many MiB "
                          "(a known-size reference for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -268,6 +353,13 @@ def main() -> int:
         "gpu": torch.cuda.get_device_name(0),
         "clock_policy": "default power mode (not pinned)",
     }
+    if not args.no_producer:
+        prod = producer_bench(cfg, args.seed)
+        rows = B * H * T
+        prod["gpu_rows_per_s"] = round(rows / ((prod["forward"]["avg_us"] + prod["backward"]["avg_us"]) * 1e-6), 1)
+        if not args.no_cpu_baseline:
+            prod["cpu_baseline"] = producer_cpu_baseline(cfg, args.seed)
+        result["producer_qk_norm_rope"] = prod
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seconds)
     print(json.dumps(result), flush=True)

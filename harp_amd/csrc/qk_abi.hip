@@ -74,6 +74,14 @@ int check_dtype(int dt, const char* name) {
   return HARP_QK_OK;
 }
 
+// the weight is read with 16-byte loads
+int check_weight(const void* w, int dt) {
+  int rc;
+  if ((rc = check_dtype(dt, "weight"))) return rc;
+  if ((reinterpret_cast<uintptr_t>(w) & 15u) != 0) return fail(HARP_QK_EINVAL, "weight must be 16-byte aligned");
+  return HARP_QK_OK;
+}
+
 Strides4 s3(const int64_t* st) { return Strides4{st[0], st[1], st[2]}; }
 
 int launched(hipError_t e, const char* what) {
@@ -81,7 +89,7 @@ int launched(hipError_t e, const char* what) {
   return HARP_QK_OK;
 }
 
-size_t bwd_ws_bytes(const QkShape& sh) { return (size_t)bwd_blocks(sh) * (size_t)sh.D * sizeof(float); }
+size_t bwd_ws_bytes(const QkShape& sh) { return bwd_workspace_floats(sh) * sizeof(float); }
 
 // Library-owned grow-only workspace per device (used when the caller passes
 // workspace == NULL); calls that overlap on one device then share it.
@@ -127,7 +135,7 @@ int forward(int mode, const void* x, const int64_t* xs, const void* weight, int 
   if ((rc = check_view(x, xs, "x"))) return rc;
   if ((rc = check_view(out, os, "out"))) return rc;
   if (mode & 1) {
-    if (weight && (rc = check_dtype(wdt, "weight"))) return rc;
+    if (weight && (rc = check_weight(weight, wdt))) return rc;
     if (!(eps >= 0.f) || eps != eps) return fail(HARP_QK_EINVAL, "eps must be a non-negative number");
   }
   if ((mode & 2) && (rc = check_freqs(freqs, fsb, fss))) return rc;
@@ -161,7 +169,7 @@ int backward(int mode, const void* dy, const int64_t* dys, const void* x, const 
   if (mode & 1) {
     if ((rc = check_view(x, xs, "input"))) return rc;
     if (!rms) return fail(HARP_QK_EINVAL, "rms is NULL");
-    if (weight && (rc = check_dtype(wdt, "weight"))) return rc;
+    if (weight && (rc = check_weight(weight, wdt))) return rc;
     if (gw && (rc = check_dtype(gwdt, "grad_weight"))) return rc;
     if ((rc = resolve_workspace(&ws, &wsb, bwd_ws_bytes(sh)))) return rc;
   }

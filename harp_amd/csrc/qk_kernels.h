@@ -41,13 +41,21 @@ struct QkBwdParams {
   const float* rms;    // saved by the forward
   const float* freqs;
   int64_t f_stride_b, f_stride_s;
-  float* wpart;        // [blocks][D] fp32 weight-gradient partials (workspace)
+  float* wpart;        // [blocks][D] fp32 weight-gradient partials, then the
+                       // reduction's group sums (workspace, bwd_workspace_floats)
 };
 
 // Blocks of the backward kernel (grid-stride over rows); bounds the
 // weight-gradient workspace to kQkBwdMaxBlocks * D floats.
 constexpr int kQkBwdMaxBlocks = 2048;
 int bwd_blocks(const QkShape& sh);
+// Partial rows per group of the first level of the weight-gradient reduction;
+// the workspace holds the partials and then one row per group.
+constexpr int kWgGroupRows = 64;
+inline size_t bwd_workspace_floats(const QkShape& sh) {
+  const size_t nblk = (size_t)bwd_blocks(sh);
+  return (nblk + (nblk + kWgGroupRows - 1) / kWgGroupRows) * (size_t)sh.D;
+}
 
 // mode: 1 = RMSNorm, 2 = RoPE, 3 = RMSNorm then RoPE (forward) /
 // RoPE backward then RMSNorm backward (backward)

@@ -48,24 +48,28 @@ __device__ __forceinline__ float row_sum16(float v) {
   return v;
 }
 
-// Position of this thread's row and chunk base.
+// Position of a thread's row.  Rows are visited with the head fastest, then
+// the token, then the batch: in the token-major layout the rows of one token
+// are one contiguous run, and they share one row of the RoPE table.  The
+// per-row rms is stored at (b*H + h)*S + s either way.
 struct RowPos {
-  int64_t row;  // linear row index over (b, h, s), in that order
+  int64_t visit;  // visit index over (b, s, h), h fastest
+  int64_t row;    // (b*H + h)*S + s
   int b, h, s;
-  int sub;      // lane within the row's 16
+  int sub;        // lane within the row's 16
   bool ok;
 };
-__device__ __forceinline__ RowPos row_pos(const QkShape& sh) {
+__device__ __forceinline__ RowPos row_at(const QkShape& sh, int64_t visit) {
   RowPos r;
-  const int64_t rows = (int64_t)sh.B * sh.H * sh.S;
-  r.row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  r.visit = visit;
   r.sub = threadIdx.x & 15;
-  r.ok = r.row < rows;
-  const int64_t rr = r.ok ? r.row : 0;
-  r.s = (int)(rr % sh.S);
-  const int64_t bh = rr / sh.S;
-  r.h = (int)(bh % sh.H);
-  r.b = (int)(bh / sh.H);
+  r.ok = visit < (int64_t)sh.B * sh.H * sh.S;
+  const int64_t v = r.ok ? visit : 0;
+  r.h = (int)(v % sh.H);
+  const int64_t bs = v / sh.H;
+  r.s = (int)(bs % sh.S);
+  r.b = (int)(bs / sh.S);
+  r.row = ((int64_t)r.b * sh.H + r.h) * sh.S + r.s;
   return r;
 }
 __device__ __forceinline__ int64_t elem_off(const Strides4& st, const RowPos& r) {
@@ -100,16 +104,28 @@ __device__ __forceinline__ void store_row(uint16_t* base, int D, int sub, const 
     }
   }
 }
-// weight (bf16 or fp32) chunk as fp32; absent weight = 1
+// weight (bf16 or fp32) chunk as fp32; absent weight = 1.  The weight is a
+// separate allocation of D elements: 16-byte loads stay inside it because D
+// is a multiple of 8 and allocations are at least 16-byte aligned.
 template <int NCH>
 __device__ __forceinline__ void load_weight(const void* w, int w_f32, int D, int sub, float (&v)[NCH][8]) {
 #pragma unroll
   for (int j = 0; j < NCH; ++j) {
     const int e0 = 8 * (16 * j + sub);
+    if (!w || e0 >= D) {
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const int e = e0 + k;
-      v[j][k] = (!w || e >= D) ? 1.f : (w_f32 ? ((const float*)w)[e] : bf16_to_f32(((const uint16_t*)w)[e]));
+      for (int k = 0; k < 8; ++k) v[j][k] = 1.f;
+    } else if (w_f32) {
+      const f32x4 a = *(const f32x4*)((const float*)w + e0), c = *(const f32x4*)((const float*)w + e0 + 4);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        v[j][k] = a[k];
+        v[j][k + 4] = c[k];
+      }
+    } else {
+      const u16x8 u = *(const u16x8*)((const uint16_t*)w + e0);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[j][k] = bf16_to_f32(u[k]);
     }
   }
 }
@@ -203,7 +219,7 @@ __device__ __forceinline__ void rmsnorm_bwd_row(const float (&x)[NCH][8], float 
 // ---------------------------------------------------------------------------
 template <int NCH, int MODE>
 __global__ __launch_bounds__(256) void qk_forward_kernel(QkFwdParams p) {
-  const RowPos r = row_pos(p.sh);
+  const RowPos r = row_at(p.sh, (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4));
   if (!r.ok) return;  // whole 16-lane groups exit together
   float v[NCH][8];
   load_row<NCH>(p.x + elem_off(p.sx, r), p.sh.D, r.sub, v);
@@ -239,15 +255,8 @@ __global__ __launch_bounds__(256) void qk_backward_kernel(QkBwdParams p) {
   float w[NCH][8];
   if (MODE & 1) load_weight<NCH>(p.weight, p.weight_f32, p.sh.D, threadIdx.x & 15, w);
   for (int64_t base = (int64_t)blockIdx.x * 16; base < rows; base += (int64_t)gridDim.x * 16) {
-    RowPos r;
-    r.row = base + (threadIdx.x >> 4);
-    r.sub = threadIdx.x & 15;
-    r.ok = r.row < rows;
+    const RowPos r = row_at(p.sh, base + (threadIdx.x >> 4));
     if (!r.ok) break;  // only the last stride has short rows; whole groups leave together
-    r.s = (int)(r.row % p.sh.S);
-    const int64_t bh = r.row / p.sh.S;
-    r.h = (int)(bh % p.sh.H);
-    r.b = (int)(bh / p.sh.H);
     float g[NCH][8];
     load_row<NCH>(p.dy + elem_off(p.sdy, r), p.sh.D, r.sub, g);
     if (MODE & 2) {
@@ -279,13 +288,33 @@ __global__ __launch_bounds__(256) void qk_backward_kernel(QkBwdParams p) {
   }
 }
 
-// grad_weight[e] = sum over blocks of wpart[block][e], stored as fp32 or bf16
-// (truncated, like the reference's other bf16 stores).
-__global__ __launch_bounds__(256) void wgrad_reduce_kernel(const float* wpart, int nblk, int D, void* gw, int gw_f32) {
+// grad_weight[e] = sum over blocks of wpart[block][e], in two levels (fixed
+// order, so the result is deterministic):
+//   level 1: block (column tile x, group y) sums the kWgGroupRows partial rows
+//   of group y for 64 columns, 4 waves each taking every 4th row, combined in
+//   LDS, into level2[y][e];
+//   level 2: one thread per column sums the groups and stores grad_weight as
+//   fp32 or bf16 (truncated, like the reference's other bf16 stores).
+__global__ __launch_bounds__(256) void wgrad_level1_kernel(const float* wpart, int nblk, int D, float* level2) {
+  __shared__ float part[4][64];
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int e = blockIdx.x * 64 + tx;
+  const int i0 = blockIdx.y * kWgGroupRows, i1 = min(i0 + kWgGroupRows, nblk);
+  float acc = 0.f;
+  if (e < D) {
+#pragma unroll 4
+    for (int i = i0 + ty; i < i1; i += 4) acc += wpart[(int64_t)i * D + e];
+  }
+  part[ty][tx] = acc;
+  __syncthreads();
+  if (ty == 0 && e < D) level2[(int64_t)blockIdx.y * D + e] = ((part[0][tx] + part[1][tx]) + part[2][tx]) + part[3][tx];
+}
+__global__ __launch_bounds__(256) void wgrad_level2_kernel(const float* level2, int ngroups, int D, void* gw,
+                                                           int gw_f32) {
   const int e = blockIdx.x * 256 + threadIdx.x;
   if (e >= D) return;
   float acc = 0.f;
-  for (int i = 0; i < nblk; ++i) acc += wpart[(int64_t)i * D + e];
+  for (int i = 0; i < ngroups; ++i) acc += level2[(int64_t)i * D + e];
   if (gw_f32) ((float*)gw)[e] = acc;
   else ((uint16_t*)gw)[e] = f32_to_bf16_trunc(acc);
 }
@@ -329,7 +358,13 @@ hipError_t launch_qk_backward(const QkBwdParams& p, int mode, hipStream_t st) {
 }
 
 hipError_t launch_wgrad_reduce(const float* wpart, int nblk, int D, void* gw, int gw_f32, hipStream_t st) {
-  hipLaunchKernelGGL(wgrad_reduce_kernel, dim3((unsigned)((D + 255) / 256)), dim3(256), 0, st, wpart, nblk, D, gw,
+  float* level2 = const_cast<float*>(wpart) + (size_t)nblk * D;
+  const int ngroups = (nblk + kWgGroupRows - 1) / kWgGroupRows;
+  hipLaunchKernelGGL(wgrad_level1_kernel, dim3((unsigned)((D + 63) / 64), (unsigned)ngroups), dim3(256), 0, st, wpart,
+                     nblk, D, level2);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(wgrad_level2_kernel, dim3((unsigned)((D + 255) / 256)), dim3(256), 0, st, level2, ngroups, D, gw,
                      gw_f32);
   return hipGetLastError();
 }

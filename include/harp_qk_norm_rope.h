@@ -13,7 +13,8 @@
  * HIP stream (NULL = default stream), int status (HARP_QK_OK = 0) and
  * harp_qk_last_error() for the message.  bf16 rows are read and written with
  * 16-byte accesses: bf16 bases 16-byte aligned, b/h/s strides multiples of 8
- * elements, D a multiple of 8 (and even, for RoPE), 8 <= D <= 256.
+ * elements, D a multiple of 8 (and even, for RoPE), 8 <= D <= 256; the RMSNorm
+ * weight (16-byte aligned) is read with 16-byte loads too.
  *
  * freqs is the RoPE table as fp32 (cos, sin) pairs: torch.view_as_real of
  * the complex [S, D/2] (or [B, S, D/2]) freqs_cis, flattened to [.., S, D];
@@ -126,7 +127,8 @@ HARP_QK_API int harp_qk_norm_rope_backward(const void* dy, const int64_t* dy_str
 
 /* Device workspace the two backward entry points with RMSNorm need
  * ((size_t)-1 when the arguments are invalid): the weight-gradient partial
- * sums, at most 2048 x h_len floats. */
+ * sums of up to 2048 row blocks and their 64-row group sums, at most
+ * (2048 + 32) x h_len floats. */
 HARP_QK_API size_t harp_qk_backward_workspace_bytes(int batch, int h_num, int s_len, int h_len);
 
 /* Last error message of the calling thread ("" if none). */

@@ -76,6 +76,7 @@ def _fwd(**over):
     (dict(fss=130), "multiples of 4"),
     (dict(eps=-1.0), "eps"),
     (dict(w=FAKE, wdt=7), "dtype"),
+    (dict(w=FAKE + 4, wdt=1), "weight must be 16-byte aligned"),
 ])
 def test_forward_rejects_bad_arguments_on_the_host(over, msg):
     rc = _fwd(**over)
@@ -89,10 +90,10 @@ def test_backward_validation_and_workspace_size():
     rc = lib.harp_qk_rmsnorm_backward(FAKE, st, FAKE, st, None, 1, None, FAKE, st, None, 1, 1, 8, 64, 128,
                                       None, 0, None)
     assert rc == 1 and "rms is NULL" in lib.harp_qk_last_error().decode()
-    # 1*8*64 rows -> 32 blocks of 16 rows, 128 floats each
-    assert lib.harp_qk_backward_workspace_bytes(1, 8, 64, 128) == 32 * 128 * 4
-    # capped at 2048 blocks
-    assert lib.harp_qk_backward_workspace_bytes(1, 24, 8192, 128) == 2048 * 128 * 4
+    # 1*8*64 rows -> 32 blocks of 16 rows (+ 1 group row), 128 floats each
+    assert lib.harp_qk_backward_workspace_bytes(1, 8, 64, 128) == (32 + 1) * 128 * 4
+    # capped at 2048 blocks (+ 32 groups of 64)
+    assert lib.harp_qk_backward_workspace_bytes(1, 24, 8192, 128) == (2048 + 32) * 128 * 4
     assert lib.harp_qk_backward_workspace_bytes(1, 8, 64, 100) == 2 ** 64 - 1
 
 
