@@ -45,8 +45,8 @@ struct QkBwdParams {
                        // reduction's group sums (workspace, bwd_workspace_floats)
 };
 
-// Blocks of the backward kernel (grid-stride over rows); bounds the
-// weight-gradient workspace to kQkBwdMaxBlocks * D floats.
+// Blocks of the backward kernel (each a contiguous range of rows); bounds the
+// weight-gradient workspace (one partial row of D floats per block).
 constexpr int kQkBwdMaxBlocks = 2048;
 int bwd_blocks(const QkShape& sh);
 // Partial rows per group of the first level of the weight-gradient reduction;

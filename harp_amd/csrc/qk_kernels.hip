@@ -59,6 +59,14 @@ struct RowPos {
   int sub;        // lane within the row's 16
   bool ok;
 };
+// Block index -> logical block with the 8 XCDs (workgroups are dealt to them
+// round-robin) each taking one contiguous range of logical blocks: the rows
+// of one token, its RoPE table row and the neighbouring rms entries of a head
+// are then fetched into, and merged in, one XCD's L2 instead of up to eight.
+__device__ __forceinline__ int64_t xcd_block(int64_t i, int64_t n) {
+  const int64_t q = n / 8, r = n % 8, x = i % 8, local = i / 8;
+  return x < r ? x * (q + 1) + local : r * (q + 1) + (x - r) * q + local;
+}
 __device__ __forceinline__ RowPos row_at(const QkShape& sh, int64_t visit) {
   RowPos r;
   r.visit = visit;
@@ -219,7 +227,7 @@ __device__ __forceinline__ void rmsnorm_bwd_row(const float (&x)[NCH][8], float 
 // ---------------------------------------------------------------------------
 template <int NCH, int MODE>
 __global__ __launch_bounds__(256) void qk_forward_kernel(QkFwdParams p) {
-  const RowPos r = row_at(p.sh, (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4));
+  const RowPos r = row_at(p.sh, xcd_block(blockIdx.x, gridDim.x) * 16 + (threadIdx.x >> 4));
   if (!r.ok) return;  // whole 16-lane groups exit together
   float v[NCH][8];
   load_row<NCH>(p.x + elem_off(p.sx, r), p.sh.D, r.sub, v);
@@ -239,9 +247,10 @@ __global__ __launch_bounds__(256) void qk_forward_kernel(QkFwdParams p) {
 
 // ---------------------------------------------------------------------------
 // Backward: MODE 1 = RMSNorm, 2 = RoPE, 3 = RoPE backward then RMSNorm
-// backward (fused).  With RMSNorm, each block walks rows with a grid stride
-// and writes its fp32 weight-gradient partial sums to wpart[block][D]; the
-// partials are summed in a second kernel (deterministic, no atomics).
+// backward (fused).  Each block walks a contiguous range of 16-row groups
+// (kQkBwdMaxBlocks blocks at most).  With RMSNorm it writes its fp32
+// weight-gradient partial sums to wpart[block][D]; the partials are summed
+// in a second kernel (deterministic, no atomics).
 // ---------------------------------------------------------------------------
 template <int NCH, int MODE>
 __global__ __launch_bounds__(256) void qk_backward_kernel(QkBwdParams p) {
@@ -254,9 +263,11 @@ __global__ __launch_bounds__(256) void qk_backward_kernel(QkBwdParams p) {
     for (int k = 0; k < 8; ++k) wg[j][k] = 0.f;
   float w[NCH][8];
   if (MODE & 1) load_weight<NCH>(p.weight, p.weight_f32, p.sh.D, threadIdx.x & 15, w);
-  for (int64_t base = (int64_t)blockIdx.x * 16; base < rows; base += (int64_t)gridDim.x * 16) {
-    const RowPos r = row_at(p.sh, base + (threadIdx.x >> 4));
-    if (!r.ok) break;  // only the last stride has short rows; whole groups leave together
+  const int64_t groups = (rows + 15) / 16, per = (groups + gridDim.x - 1) / gridDim.x;
+  const int64_t g0 = xcd_block(blockIdx.x, gridDim.x) * per, g1 = min(g0 + per, groups);
+  for (int64_t gi = g0; gi < g1; ++gi) {
+    const RowPos r = row_at(p.sh, gi * 16 + (threadIdx.x >> 4));
+    if (!r.ok) break;  // only the last group has short rows; whole 16-lane groups leave together
     float g[NCH][8];
     load_row<NCH>(p.dy + elem_off(p.sdy, r), p.sh.D, r.sub, g);
     if (MODE & 2) {
@@ -288,35 +299,37 @@ __global__ __launch_bounds__(256) void qk_backward_kernel(QkBwdParams p) {
   }
 }
 
-// grad_weight[e] = sum over blocks of wpart[block][e], in two levels (fixed
-// order, so the result is deterministic):
-//   level 1: block (column tile x, group y) sums the kWgGroupRows partial rows
-//   of group y for 64 columns, 4 waves each taking every 4th row, combined in
-//   LDS, into level2[y][e];
-//   level 2: one thread per column sums the groups and stores grad_weight as
-//   fp32 or bf16 (truncated, like the reference's other bf16 stores).
-__global__ __launch_bounds__(256) void wgrad_level1_kernel(const float* wpart, int nblk, int D, float* level2) {
-  __shared__ float part[4][64];
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-  const int e = blockIdx.x * 64 + tx;
-  const int i0 = blockIdx.y * kWgGroupRows, i1 = min(i0 + kWgGroupRows, nblk);
+// grad_weight[e] = sum over blocks of wpart[block][e], in two launches of the
+// kernel below with a fixed order (so the result is deterministic): level 1
+// sums groups of kWgGroupRows partial rows into level2[group][e], level 2 sums
+// the groups and stores grad_weight as fp32 or bf16 (truncated, like the
+// reference's other bf16 stores).  Two small launches over many CUs beat one
+// launch over a few: a CU's own fetch rate bounds a single block.
+//
+// Block (x, g) sums rows [g*group_rows, (g+1)*group_rows) of src[nrows][D] for
+// columns 16x .. 16x+15: its 16 row lanes take every 16th row (64-byte row
+// segments, independent loads in flight) and LDS adds the lane sums in order.
+template <bool FINAL>
+__global__ __launch_bounds__(256) void wgrad_sum_kernel(const float* src, int nrows, int group_rows, int D, void* dst,
+                                                        int dst_f32) {
+  __shared__ float part[16][17];
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+  const int e = blockIdx.x * 16 + tx;
+  const int i0 = blockIdx.y * group_rows, i1 = min(i0 + group_rows, nrows);
   float acc = 0.f;
   if (e < D) {
 #pragma unroll 4
-    for (int i = i0 + ty; i < i1; i += 4) acc += wpart[(int64_t)i * D + e];
+    for (int i = i0 + ty; i < i1; i += 16) acc += src[(int64_t)i * D + e];
   }
   part[ty][tx] = acc;
   __syncthreads();
-  if (ty == 0 && e < D) level2[(int64_t)blockIdx.y * D + e] = ((part[0][tx] + part[1][tx]) + part[2][tx]) + part[3][tx];
-}
-__global__ __launch_bounds__(256) void wgrad_level2_kernel(const float* level2, int ngroups, int D, void* gw,
-                                                           int gw_f32) {
-  const int e = blockIdx.x * 256 + threadIdx.x;
-  if (e >= D) return;
-  float acc = 0.f;
-  for (int i = 0; i < ngroups; ++i) acc += level2[(int64_t)i * D + e];
-  if (gw_f32) ((float*)gw)[e] = acc;
-  else ((uint16_t*)gw)[e] = f32_to_bf16_trunc(acc);
+  if (ty != 0 || e >= D) return;
+  float v = 0.f;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) v += part[k][tx];
+  if (!FINAL) ((float*)dst)[(int64_t)blockIdx.y * D + e] = v;
+  else if (dst_f32) ((float*)dst)[e] = v;
+  else ((uint16_t*)dst)[e] = f32_to_bf16_trunc(v);
 }
 
 // ---------------------------------------------------------------------------
@@ -360,12 +373,13 @@ hipError_t launch_qk_backward(const QkBwdParams& p, int mode, hipStream_t st) {
 hipError_t launch_wgrad_reduce(const float* wpart, int nblk, int D, void* gw, int gw_f32, hipStream_t st) {
   float* level2 = const_cast<float*>(wpart) + (size_t)nblk * D;
   const int ngroups = (nblk + kWgGroupRows - 1) / kWgGroupRows;
-  hipLaunchKernelGGL(wgrad_level1_kernel, dim3((unsigned)((D + 63) / 64), (unsigned)ngroups), dim3(256), 0, st, wpart,
-                     nblk, D, level2);
+  const unsigned cols = (unsigned)((D + 15) / 16);
+  hipLaunchKernelGGL(wgrad_sum_kernel<false>, dim3(cols, (unsigned)ngroups), dim3(256), 0, st, wpart, nblk,
+                     kWgGroupRows, D, (void*)level2, 1);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(wgrad_level2_kernel, dim3((unsigned)((D + 255) / 256)), dim3(256), 0, st, level2, ngroups, D, gw,
-                     gw_f32);
+  hipLaunchKernelGGL(wgrad_sum_kernel<true>, dim3(cols, 1u), dim3(256), 0, st, (const float*)level2, ngroups, ngroups,
+                     D, gw, gw_f32);
   return hipGetLastError();
 }
 

@@ -11,9 +11,10 @@
 //   qk_norm_rope_forward(x, weight, freqs_cis, output!, rms!, eps)
 //   qk_norm_rope_backward(input, grad_output, weight, rms, freqs_cis,
 //                         grad_input!, grad_weight!)
-// The reference registers these for the CPU key of its own async_op library;
-// this library is loaded instead of it for GPU tensors (the two define the
-// same namespace and cannot be loaded into one process together).
+// The reference registers these for the CPU key of its own async_op library
+// (an aarch64 build).  This one defines them as a fragment of the namespace,
+// so a library holding the namespace's other operators (silu, tanh, add, ...)
+// can be loaded next to it, as long as it does not define these six names.
 //
 // Implementations are registered for the CUDA dispatch key (PyTorch-ROCm
 // tensors on a HIP device carry it) and call libharp_ra.so through
@@ -249,7 +250,7 @@ void qk_norm_rope_backward_cpu(const at::Tensor&, const at::Tensor&, const at::T
 
 }  // namespace
 
-TORCH_LIBRARY(async_op, m) {
+TORCH_LIBRARY_FRAGMENT(async_op, m) {
   m.def("rmsnorm_forward_out(Tensor input, Tensor weight, Tensor(a!) output, Tensor(b!) rms, float eps) -> ()");
   m.def(
       "rmsnorm_backward_out(Tensor input, Tensor grad_output, Tensor weight, Tensor rms, Tensor(a!) grad_input, "

@@ -109,3 +109,17 @@ def test_cpu_tensors_are_refused():
     x = torch.zeros(1, 2, 3, 64, dtype=torch.bfloat16)
     with pytest.raises(RuntimeError, match="HIP device only"):
         torch.ops.async_op.rope_forward_impl(x, torch.zeros(3, 32, dtype=torch.complex64), x)
+
+
+def test_namespace_is_shared_with_another_library():
+    """The operators are a fragment of async_op: a library that defines the
+    namespace's other operators (as the reference's own async_op library
+    does for silu, tanh, add, ...) loads next to this one."""
+    harp_amd.load_async_ops()
+    other = torch.library.Library("async_op", "DEF")
+    try:
+        other.define("silu_out(Tensor input, Tensor(a!) output) -> ()")
+        assert str(torch.ops.async_op.silu_out.default._schema).startswith("async_op::silu_out")
+        assert str(torch.ops.async_op.rope_forward_impl.default._schema) == "async_op::" + REF_SCHEMAS["rope_forward_impl"]
+    finally:
+        other._destroy()
