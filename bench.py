@@ -180,6 +180,35 @@ def producer_bench(cfg, seed: int, iters: int = 20):
                      "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
     res["shape"] = f"[B,H,T,D]=[{B},{H},{T},{D}] token-major bf16, weight bf16 [D], freqs complex64 [T, D/2]"
     res["ops"] = "async_op.qk_norm_rope_forward / qk_norm_rope_backward (one of Q, K)"
+
+    # The whole producer of one rank's q, k, v (harp_amd.project_qkv): three
+    # projections of hidden [B, T, H*D] (plain library GEMMs, hipBLASLt) and
+    # the fused norm + RoPE of q and k, forward only.
+    from types import SimpleNamespace
+
+    dim = H * D
+    lin = [torch.nn.Linear(dim, dim, bias=False).to(dev, torch.bfloat16) for _ in range(3)]
+    norm = SimpleNamespace(weight=w, eps=1e-6)
+    attn = SimpleNamespace(heads=H, to_q=lin[0], to_k=lin[1], to_v=lin[2], norm_q=norm, norm_k=norm)
+    hid = torch.randn((B, T, dim), generator=g).to(torch.bfloat16).to(dev)
+    with torch.no_grad():
+        for _ in range(3):
+            harp_amd.project_qkv(attn, hid, freqs)
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        torch.cuda.synchronize()
+        ev[0].record()
+        for _ in range(iters):
+            harp_amd.project_qkv(attn, hid, freqs)
+        ev[1].record()
+        torch.cuda.synchronize()
+    ms = ev[0].elapsed_time(ev[1]) / iters
+    gemm_flop = 3 * 2 * B * T * dim * dim
+    res["project_qkv_forward"] = {
+        "avg_ms": round(ms, 4),
+        "gemm_flop": gemm_flop,
+        "tflops_incl_norm_rope": round(gemm_flop / (ms * 1e-3) / 1e12, 1),
+        "what": f"3 projections [{B},{T},{dim}] x [{dim},{dim}] (torch Linear, hipBLASLt) + fused norm+RoPE of q and k",
+    }
     return res
 
 

@@ -5,7 +5,9 @@ hand-written HIP kernels behind the C ABI of ``include/harp_ring_attn.h``
 (``kernels/libharp_ra.so``) and a PyTorch-ROCm operator library
 (``kernels/libring_attention_ops.so``).  The step before it, QK RMSNorm and the
 rotary embedding, runs on the GPU too (``include/harp_qk_norm_rope.h``,
-``kernels/libharp_async_op.so``, namespace ``async_op``).  Build with
+``kernels/libharp_async_op.so``, namespace ``async_op``), and
+:class:`RingZAttention` wires projections, QK norm, RoPE, ring attention and
+the output projection as the model's attention block does.  Build with
 ``python -m harp_amd.build``.
 """
 
@@ -21,6 +23,7 @@ from .ops import (  # noqa: F401
     ring_attention,
 )
 from .qk import ApplyRotaryComplexFn, QKNormRopeFn, RMSNormFn  # noqa: F401
+from .attention import RingZAttention, project_qkv  # noqa: F401
 from .wait_engine import CommWork, WaitEngine  # noqa: F401
 
 __version__ = "0.1.0"
