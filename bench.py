@@ -130,7 +130,7 @@ def cpu_baseline(cfg, target_s: float):
 
 
 def producer_bench(cfg, seed: int, iters: int = 20):
-    """The step before the path: fused QK RMSNorm + RoPE
+    """The step before the ring-attention block: fused QK RMSNorm + RoPE
     forward and backward (torch.ops.async_op.qk_norm_rope_{forward,backward})
     on one Q-shaped tensor of the workload ([B, H, T, D] token-major view),
     timed with HIP events on the current stream.  HBM-bound: algorithmic

@@ -4,8 +4,8 @@
 // Host flow mirrors the reference operators (async_rt/csrc/rms_norm.cc:447-522,
 // async_rt/csrc/rope.cc:186-249): the reference walks rows on CPU threads
 // (at::parallel_for); here one launch covers every row of every head, and the
-// RMSNorm weight gradient is reduced from per-block partial sums by a second
-// small launch instead of per-thread buffers.
+// RMSNorm weight gradient is reduced from per-block partial sums by two small
+// launches instead of per-thread buffers.
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
