@@ -53,6 +53,11 @@ HIPCC_FLAGS = [
     "-Xclang",
     "-packed-fp32-ops",
     "-Wno-unused-command-line-argument",
+    # machine scheduler aiming at instruction-level parallelism within the
+    # regions the kernels' scheduling fences leave it: 0.4% faster step than
+    # the default strategy at the headline shape, same register use
+    "-mllvm",
+    "-amdgpu-sched-strategy=max-ilp",
 ]
 
 
