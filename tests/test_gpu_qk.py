@@ -197,6 +197,31 @@ def test_fused_ops_equal_the_composition(B, H, S, D, layout, wk, batched):
         assert_bf16_close(bits(gw), qo.f32_to_bf16_trunc(want_gw), max_frac=0.05, what="grad_weight bf16")
 
 
+@pytest.mark.parametrize("D", [8, 16, 24, 40, 72, 120, 136, 200, 248])
+def test_head_dim_sweep(D):
+    """Every head dim class of the kernels: one 16-byte chunk per lane, a
+    partial first chunk set (D < 128), and a partial second one (D > 128)."""
+    B, H, S = 1, 3, 40
+    o = ops()
+    x, xb = make_x(B, H, S, D, "token", seed=D, scale=1.5)
+    w, wb = make_w(D, "f32", seed=D + 1)
+    fc, f_np = freqs_cis(S, D)
+    eps = 1e-6
+    y = torch.empty_like(x)
+    rms = torch.empty(B * H * S, device=DEV, dtype=torch.float32)
+    o.qk_norm_rope_forward(x, w, fc, y, rms, eps)
+    want, want_rms = qo.norm_rope_forward(xb, wb, eps, f_np)
+    assert_pairs_close(bits(y), want, what=f"D={D} fused fwd")
+    np.testing.assert_allclose(rms.cpu().numpy(), want_rms.reshape(-1), rtol=1e-6)
+    dy, dyb = make_x(B, H, S, D, "token", seed=D + 2)
+    dx = torch.empty_like(x)
+    gw = torch.empty(D, device=DEV, dtype=torch.float32)
+    o.qk_norm_rope_backward(x, dy, w, rms, fc, dx, gw)
+    want_dx, want_gw = qo.norm_rope_backward(xb, dyb, wb, rms.cpu().numpy().reshape(B, H, S), f_np)
+    assert_grad_close(bits(dx), want_dx, what=f"D={D} fused bwd")
+    np.testing.assert_allclose(gw.cpu().numpy(), want_gw, rtol=1e-5, atol=1e-5 * np.abs(want_gw).max())
+
+
 def test_in_place_and_head_major_output():
     o = ops()
     B, H, S, D = 1, 6, 130, 128
