@@ -123,3 +123,25 @@ def test_namespace_is_shared_with_another_library():
         assert str(torch.ops.async_op.rope_forward_impl.default._schema) == "async_op::" + REF_SCHEMAS["rope_forward_impl"]
     finally:
         other._destroy()
+
+
+def test_attention_block_on_cpu_tensors_raises():
+    """The block module has no CPU path either: its first GPU operator
+    (the fused QK norm + RoPE) refuses CPU tensors."""
+    from torch import nn
+
+    attn = nn.Module()
+    attn.heads = 2
+    attn.to_q, attn.to_k, attn.to_v = (nn.Linear(128, 128, bias=False).to(torch.bfloat16) for _ in range(3))
+    attn.to_out = nn.ModuleList([nn.Linear(128, 128, bias=False).to(torch.bfloat16)])
+    norm = nn.Module()
+    norm.weight = nn.Parameter(torch.ones(64, dtype=torch.bfloat16))
+    norm.eps = 1e-5
+    attn.norm_q = attn.norm_k = norm
+    block = harp_amd.RingZAttention(attn, 2)
+    x = torch.zeros(1, 32, 128, dtype=torch.bfloat16)
+    freqs = torch.polar(torch.ones(32, 32), torch.zeros(32, 32))
+    with pytest.raises(RuntimeError, match="HIP device only"):
+        block(x, freqs)
+    with pytest.raises(ValueError, match="multiple of sp_size"):
+        harp_amd.RingZAttention(attn, 3)(x, freqs)
