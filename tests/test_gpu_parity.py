@@ -329,3 +329,41 @@ def test_config2_robustness_seeds(seed):
     res = run_hip(q, ks, vs, do, 0.125)
     ref = _oracle_full(q, ks, vs, do, 0.125, dtype=torch.float32)
     _check_all(res, ref)
+
+
+# --- randomized shapes ------------------------------------------------------------
+
+def _random_cases(n=16, seed=2024):
+    """Deterministic random problems: batch, heads, query rows, head dim,
+    chunk count and length, valid length per chunk (some chunks ragged or
+    empty, at least one key overall), ring rank, value scale."""
+    g = torch.Generator().manual_seed(seed)
+
+    def ri(lo, hi):
+        return int(torch.randint(lo, hi + 1, (1,), generator=g))
+
+    cases = []
+    for i in range(n):
+        B, H, T = ri(1, 2), ri(1, 4), ri(1, 300)
+        D = 8 * ri(1, 16)
+        N = ri(1, 5)
+        tc = ri(1, 260)
+        lens = [ri(0, tc) if ri(0, 2) else tc for _ in range(N)]
+        if sum(lens) == 0:
+            lens[0] = tc
+        cases.append((i, B, H, T, D, N, tc, lens, ri(0, N - 1), [0.5, 1.0, 2.0][ri(0, 2)]))
+    return cases
+
+
+@pytest.mark.parametrize("case", _random_cases(), ids=lambda c: f"r{c[0]}")
+def test_random_shapes(case):
+    """Random sizes against the full fp64 oracle: queries and chunks not
+    multiples of any tile, ragged and empty chunks, any ring rank."""
+    i, B, H, T, D, N, tc, lens, rank, vscale = case
+    print(f"[random r{i}: B={B} H={H} T={T} D={D} N={N} chunk={tc} lens={lens} rank={rank} x{vscale}]",
+          flush=True)
+    q, ks, vs, do = orc.make_inputs(B, H, T, D, N, seed=500 + i, value_scale=vscale, chunk_len=tc)
+    scale = 1.0 / math.sqrt(D)
+    res = run_hip(q, ks, vs, do, scale, ring_rank=rank, kv_lens=lens, via="ops" if i % 2 else "abi")
+    ref = _oracle_full(q, ks, vs, do, scale, rank=rank, lens=lens)
+    _check_all(res, ref)
