@@ -76,22 +76,55 @@ def cpu_threads() -> int:
     return max(1, n)
 
 
-def cpu_model() -> str:
+def cpu_info() -> dict:
+    """Host CPU as lscpu reports it: model, physical cores (sockets x cores per
+    socket), hardware threads, and the bf16 / matrix extensions the CPU
+    baseline's matmuls could use."""
+    info = {"model": "unknown", "physical_cores": None, "hw_threads": os.cpu_count(), "bf16_flags": []}
+    fields = {}
     try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
-    except OSError:
+        import subprocess
+
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+        for line in out.splitlines():
+            if ":" in line:
+                k, v = line.split(":", 1)
+                fields[k.strip()] = v.strip()
+    except (OSError, ValueError):
         pass
-    return "unknown"
+    flags = fields.get("Flags", "").split()
+    if not flags:
+        try:
+            with open("/proc/cpuinfo") as f:
+                for line in f:
+                    if line.startswith("flags"):
+                        flags = line.split(":", 1)[1].split()
+                        break
+        except OSError:
+            pass
+    info["model"] = fields.get("Model name", info["model"])
+    try:
+        info["physical_cores"] = int(fields["Socket(s)"]) * int(fields["Core(s) per socket"])
+        info["hw_threads"] = int(fields.get("CPU(s)", info["hw_threads"]))
+    except (KeyError, ValueError):
+        pass
+    info["bf16_flags"] = sorted(f for f in flags if f in ("avx512f", "avx512_bf16", "amx_bf16", "amx_tile", "avx_vnni"))
+    return info
+
+
+def cpu_model() -> str:
+    return cpu_info()["model"]
 
 
 def cpu_baseline(cfg, target_s: float):
     """The reference algorithm as PyTorch CPU ops (oracle.cpu_baseline_fwd_bwd)
     on a bounded sample of the workload: query rows of one head (then whole
     heads, one at a time) against the full KV length, sized from a short probe
-    to take about target_s.  Returns the cpu_baseline JSON object."""
+    so that one repetition takes about target_s / 4.  One warm-up and three
+    timed repetitions of that sample; the median is reported (BASELINE.md
+    section 5).  Returns the cpu_baseline JSON object."""
+    import statistics
+
     import torch
 
     from oracle import ring_attn_oracle as orc
@@ -112,20 +145,33 @@ def cpu_baseline(cfg, target_s: float):
         return time.perf_counter() - t0
 
     run(64, 1)  # warm up oneDNN / thread pool
-    rows_target = 128 * target_s / max(run(128, 1), 1e-3)
+    rep_s = target_s / 4
+    rows_target = 128 * rep_s / max(run(128, 1), 1e-3)
     if rows_target <= T:
         tq, nh = max(128, int(rows_target) // 128 * 128), 1
     else:
         tq, nh = T, int(min(H, max(1, rows_target // T)))
-    dt = sum(run(tq, 1 + i) for i in range(nh))
+
+    def sample():
+        return sum(run(tq, 1 + i) for i in range(nh))
+
+    sample()  # warm-up repetition
+    reps = [sample() for _ in range(3)]
+    dt = statistics.median(reps)
     flops = 14.0 * nh * tq * L * D
+    ci = cpu_info()
     return {
         "value": round(flops / dt / 1e12, 4),
         "unit": "TFLOP/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"{nh} of {H} heads x {tq} of {T} query rows against all {L} keys "
-                   f"({N} chunks), fwd+bwd, {dt:.1f} s on {cpu_model()}"),
+        "cpu_model": ci["model"],
+        "physical_cores": ci["physical_cores"],
+        "hw_threads": ci["hw_threads"],
+        "bf16_flags": ci["bf16_flags"],
+        "reps_s": [round(r, 2) for r in reps],
+        "sample": (f"{nh} of {H} heads x {tq} of {T} query rows against all {L} keys ({N} chunks), fwd+bwd; "
+                   f"median of 3 repetitions ({dt:.1f} s each) after 1 warm-up, {threads} threads"),
     }
 
 
@@ -287,9 +333,9 @@ def main() -> int:
     dv = torch.empty_like(v)
 
     def step():
-        ops.ring_attention_forward(q, k, v, out, m_i, l_i, N, scale, 0, lens)
+        ops.ring_attention_forward(q, k, v, out, m_i, l_i, N, scale, 0, lens, tc)
         delta = ops.ring_attention_delta(do, out)
-        ops.ring_attention_backward(q, dq, k, dk, v, dv, do, m_i, l_i, delta, N, scale, 0, lens)
+        ops.ring_attention_backward(q, dq, k, dk, v, dv, do, m_i, l_i, delta, N, scale, 0, lens, tc)
 
     if args.copy_calibration_mib > 0:
         n = args.copy_calibration_mib * (1 << 20) // 4
@@ -326,6 +372,11 @@ def main() -> int:
     tflops = flop_total / (ms_per_step * 1e-3) / 1e12
     # algorithmic MFMA work per launch in this design's accounting
     kernel_flops = {"fwd": 4.0 * bhtld, "dkdv": 8.0 * bhtld, "dq": 2.0 * bhtld}
+    # MFMA work each kernel performs (dq recomputes S and dP: 4 more units)
+    kernel_mfma = {"fwd": 4.0 * bhtld, "dkdv": 8.0 * bhtld, "dq": 6.0 * bhtld}
+    # sustained MFMA rate of this board (register-fed bf16 MFMA stream on
+    # random operands): what the power limit lets any MFMA-bound kernel reach
+    probe_tf, probe_ghz = _lib.probe_mfma_rate(4096, args.seed)
     kernels = {}
     for name, (ms, n) in kt.items():
         if n:
@@ -333,10 +384,10 @@ def main() -> int:
             entry = {"avg_ms": round(avg, 4), "launches_per_step": n / args.steps}
             if name in kernel_flops:
                 entry["tflops_algorithmic"] = round(kernel_flops[name] / (avg * 1e-3) / 1e12, 1)
+                performed = kernel_mfma[name] / (avg * 1e-3) / 1e12
+                entry["tflops_mfma_performed"] = round(performed, 1)
+                entry["frac_of_sustained"] = round(performed / probe_tf, 4) if probe_tf > 0 else None
             kernels[name] = entry
-    # sustained MFMA rate of this board (register-fed bf16 MFMA stream on
-    # random operands): what the power limit lets any MFMA-bound kernel reach
-    probe_tf, probe_ghz = _lib.probe_mfma_rate(4096, args.seed)
     dom = max((n for n in kernel_flops if n in kernels), key=lambda n: kt[n][0])
     dom_tf = kernels[dom]["tflops_algorithmic"]
     fwd_ms = kt["fwd"][0] / args.steps

@@ -21,6 +21,7 @@ KERNELS = ROOT / "kernels"
 ABI_LIB = KERNELS / "libharp_ra.so"
 OPS_LIB = KERNELS / "libring_attention_ops.so"
 ASYNC_OPS_LIB = KERNELS / "libharp_async_op.so"
+PROBE_LIB = KERNELS / "libharp_probe.so"  # bench-only measurement aid, not a drop-in library
 
 HARP_RA_OK = 0
 HARP_RA_EINVAL = 1
@@ -34,6 +35,7 @@ KERNEL_KINDS = ("pack", "fwd", "delta", "dkdv", "dq")
 
 _lock = threading.Lock()
 _abi: ctypes.CDLL | None = None
+_probe: ctypes.CDLL | None = None
 _ops_loaded = False
 _async_ops_loaded = False
 
@@ -62,8 +64,6 @@ ABI_PROTOTYPES = {
     "harp_ra_backward_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i, _i32p]),
     "harp_ra_timing_enable": (_i, [_i]),
     "harp_ra_timing_read": (_i, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int), _i]),
-    "harp_ra_probe_mfma_rate": (_i, [_i, ctypes.c_uint32, ctypes.POINTER(ctypes.c_double),
-                                     ctypes.POINTER(ctypes.c_double)]),
     "harp_ra_last_error": (ctypes.c_char_p, []),
     "harp_ra_version": (ctypes.c_char_p, []),
 }
@@ -162,13 +162,32 @@ def i32_array(vals) -> ctypes.Array:
     return (ctypes.c_int32 * len(vals))(*[int(v) for v in vals])
 
 
+def load_probe() -> ctypes.CDLL:
+    """Open kernels/libharp_probe.so, the bench-only sustained-MFMA probe."""
+    global _probe
+    with _lock:
+        if _probe is None:
+            if not PROBE_LIB.exists():
+                raise _missing(PROBE_LIB)
+            lib = ctypes.CDLL(str(PROBE_LIB))
+            lib.harp_probe_mfma_rate.restype = _i
+            lib.harp_probe_mfma_rate.argtypes = [_i, ctypes.c_uint32, ctypes.POINTER(ctypes.c_double),
+                                                 ctypes.POINTER(ctypes.c_double)]
+            lib.harp_probe_last_error.restype = ctypes.c_char_p
+            lib.harp_probe_last_error.argtypes = []
+            _probe = lib
+        return _probe
+
+
 def probe_mfma_rate(iters: int = 4096, seed: int = 3407) -> tuple:
     """(TFLOP/s, shader GHz) of a register-fed bf16 MFMA stream on random
     operands: the sustained MFMA rate of this device under its power limit."""
+    lib = load_probe()
     tf = ctypes.c_double()
     ghz = ctypes.c_double()
-    check(load_abi().harp_ra_probe_mfma_rate(int(iters), int(seed) & 0xFFFFFFFF, ctypes.byref(tf), ctypes.byref(ghz)),
-          "harp_ra_probe_mfma_rate")
+    rc = lib.harp_probe_mfma_rate(int(iters), int(seed) & 0xFFFFFFFF, ctypes.byref(tf), ctypes.byref(ghz))
+    if rc != 0:
+        raise RuntimeError(f"harp_probe_mfma_rate failed (status {rc}): {lib.harp_probe_last_error().decode()}")
     return tf.value, ghz.value
 
 

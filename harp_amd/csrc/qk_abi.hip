@@ -13,6 +13,7 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "../../include/harp_qk_norm_rope.h"
 #include "qk_kernels.h"
@@ -91,18 +92,28 @@ int launched(hipError_t e, const char* what) {
 
 size_t bwd_ws_bytes(const QkShape& sh) { return bwd_workspace_floats(sh) * sizeof(float); }
 
-// Library-owned grow-only workspace per device (used when the caller passes
-// workspace == NULL); calls that overlap on one device then share it.
+// Library-owned grow-only workspace for callers that pass workspace == NULL,
+// one buffer per (device, stream): calls on one stream run in order and so
+// never overlap on their buffer, and calls on different streams never share
+// one.  A buffer that must grow is freed only after its stream has drained
+// (earlier calls may still read it).  This path calls hipMalloc / hipFree, so
+// it cannot be captured into a HIP graph; callers that capture pass their own
+// workspace.
 struct OwnedWorkspace {
+  struct Buf {
+    int dev;
+    hipStream_t stream;
+    void* ptr;
+    size_t bytes;
+  };
   std::mutex mu;
-  void* ptr[64] = {};
-  size_t bytes[64] = {};
+  std::vector<Buf> bufs;
 };
 OwnedWorkspace& owned() {
   static OwnedWorkspace w;
   return w;
 }
-int resolve_workspace(void** ws, size_t* ws_bytes, size_t need) {
+int resolve_workspace(void** ws, size_t* ws_bytes, size_t need, hipStream_t stream) {
   if (*ws) {
     if (*ws_bytes < need)
       return fail(HARP_QK_ENOMEM, "workspace of %zu bytes is smaller than the %zu bytes needed", *ws_bytes, need);
@@ -110,20 +121,30 @@ int resolve_workspace(void** ws, size_t* ws_bytes, size_t need) {
     return HARP_QK_OK;
   }
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return fail(HARP_QK_ELAUNCH, "hipGetDevice failed");
+  if (hipGetDevice(&dev) != hipSuccess) return fail(HARP_QK_ELAUNCH, "hipGetDevice failed");
   OwnedWorkspace& w = owned();
   std::lock_guard<std::mutex> lk(w.mu);
-  if (w.bytes[dev] < need) {
-    if (w.ptr[dev]) (void)hipFree(w.ptr[dev]);
-    w.ptr[dev] = nullptr;
-    w.bytes[dev] = 0;
+  OwnedWorkspace::Buf* b = nullptr;
+  for (auto& x : w.bufs)
+    if (x.dev == dev && x.stream == stream) b = &x;
+  if (!b) {
+    w.bufs.push_back(OwnedWorkspace::Buf{dev, stream, nullptr, 0});
+    b = &w.bufs.back();
+  }
+  if (b->bytes < need) {
+    if (b->ptr) {
+      if (hipStreamSynchronize(stream) != hipSuccess) return fail(HARP_QK_ELAUNCH, "hipStreamSynchronize failed");
+      (void)hipFree(b->ptr);
+      b->ptr = nullptr;
+      b->bytes = 0;
+    }
     void* p = nullptr;
     if (hipMalloc(&p, need) != hipSuccess) return fail(HARP_QK_ENOMEM, "hipMalloc of %zu workspace bytes failed", need);
-    w.ptr[dev] = p;
-    w.bytes[dev] = need;
+    b->ptr = p;
+    b->bytes = need;
   }
-  *ws = w.ptr[dev];
-  *ws_bytes = w.bytes[dev];
+  *ws = b->ptr;
+  *ws_bytes = b->bytes;
   return HARP_QK_OK;
 }
 
@@ -171,7 +192,7 @@ int backward(int mode, const void* dy, const int64_t* dys, const void* x, const 
     if (!rms) return fail(HARP_QK_EINVAL, "rms is NULL");
     if (weight && (rc = check_weight(weight, wdt))) return rc;
     if (gw && (rc = check_dtype(gwdt, "grad_weight"))) return rc;
-    if ((rc = resolve_workspace(&ws, &wsb, bwd_ws_bytes(sh)))) return rc;
+    if ((rc = resolve_workspace(&ws, &wsb, bwd_ws_bytes(sh), static_cast<hipStream_t>(stream)))) return rc;
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
   QkBwdParams p;

@@ -19,6 +19,7 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "../../include/harp_ring_attn.h"
@@ -49,8 +50,11 @@ int ok() {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// bf16 operand that is read with 16-byte vector loads
-int check_bf16_view(const void* p, const int64_t* s, const char* name) {
+// bf16 operand that is read with 16-byte vector loads.  Its rows are walked
+// through buffer ranges of rows x row stride, so a row stride below D (0 for
+// an expanded view) would cut every row short: rejected.  B and H strides may
+// be 0 (a broadcast input).
+int check_bf16_view(const void* p, const int64_t* s, int D, const char* name) {
   if (!p) return fail(HARP_RA_EINVAL, "%s is NULL", name);
   if (!s) return fail(HARP_RA_EINVAL, "%s strides are NULL", name);
   if (!aligned16(p)) return fail(HARP_RA_EINVAL, "%s must be 16-byte aligned", name);
@@ -59,16 +63,44 @@ int check_bf16_view(const void* p, const int64_t* s, const char* name) {
     if (s[i] < 0 || s[i] % 8 != 0)
       return fail(HARP_RA_EINVAL, "%s stride[%d]=%lld must be a non-negative multiple of 8 elements", name, i,
                   (long long)s[i]);
+  if (s[2] < D)
+    return fail(HARP_RA_EINVAL, "%s row stride %lld is below D=%d: rows would overlap", name, (long long)s[2], D);
   return HARP_RA_OK;
 }
 
-// scalar-stored / scalar-read operand
+// fp32 input read element by element (the forward's out, for the delta)
 int check_plain_view(const void* p, const int64_t* s, const char* name) {
   if (!p) return fail(HARP_RA_EINVAL, "%s is NULL", name);
   if (!s) return fail(HARP_RA_EINVAL, "%s strides are NULL", name);
   if (s[3] != 1) return fail(HARP_RA_EINVAL, "%s must have unit stride in D (got %lld)", name, (long long)s[3]);
   for (int i = 0; i < 3; ++i)
     if (s[i] < 0) return fail(HARP_RA_EINVAL, "%s stride[%d] must be non-negative", name, i);
+  return HARP_RA_OK;
+}
+
+// Output view [B, H, rows, D] written element by element: unit D stride, and
+// no two elements at one address (else stores from different threads race).
+// Sufficient test: with the dims of extent > 1 sorted by stride, each stride
+// exceeds the span of the smaller ones.
+int check_out_view(const void* p, const int64_t* s, int B, int H, int rows, int D, const char* name) {
+  if (!p) return fail(HARP_RA_EINVAL, "%s is NULL", name);
+  if (!s) return fail(HARP_RA_EINVAL, "%s strides are NULL", name);
+  if (s[3] != 1) return fail(HARP_RA_EINVAL, "%s must have unit stride in D (got %lld)", name, (long long)s[3]);
+  for (int i = 0; i < 3; ++i)
+    if (s[i] < 0) return fail(HARP_RA_EINVAL, "%s stride[%d] must be non-negative", name, i);
+  const int64_t ext[4] = {B, H, rows, D};
+  int idx[4], n = 0;
+  for (int i = 0; i < 4; ++i)
+    if (ext[i] > 1) idx[n++] = i;
+  for (int i = 1; i < n; ++i)  // insertion sort by stride
+    for (int j = i; j > 0 && s[idx[j]] < s[idx[j - 1]]; --j) std::swap(idx[j], idx[j - 1]);
+  int64_t span = 0;  // largest offset reachable through the dims so far
+  for (int i = 0; i < n; ++i) {
+    if (s[idx[i]] <= span)
+      return fail(HARP_RA_EINVAL, "%s strides make elements overlap (stride[%d]=%lld)", name, idx[i],
+                  (long long)s[idx[i]]);
+    span += (ext[idx[i]] - 1) * s[idx[i]];
+  }
   return HARP_RA_OK;
 }
 
@@ -245,56 +277,6 @@ int harp_ra_timing_read(double* ms, int* launches, int n_kinds) {
   return ok();
 }
 
-int harp_ra_probe_mfma_rate(int iters, uint32_t seed, double* tflops, double* shader_ghz) {
-  if (!tflops || !shader_ghz) return fail(HARP_RA_EINVAL, "probe outputs are NULL");
-  if (iters < 16 || iters > (1 << 20)) return fail(HARP_RA_EINVAL, "iters=%d must be in [16, 2^20]", iters);
-  int dev = 0, cus = 0, wall_khz = 0;
-  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) ||
-      hipDeviceGetAttribute(&wall_khz, hipDeviceAttributeWallClockRate, dev) || cus < 1 || wall_khz < 1)
-    return fail(HARP_RA_ELAUNCH, "device query failed");
-  const int blocks = 8 * cus;  // 32 waves per CU, 8 per SIMD
-  float* sink = nullptr;
-  long long* clocks = nullptr;
-  hipEvent_t e0 = nullptr, e1 = nullptr;
-  int rc = HARP_RA_OK;
-  std::vector<long long> h(2 * (size_t)blocks);
-  float best_ms = 0.f;
-  if (hipMalloc(&sink, sizeof(float) * 256 * (size_t)blocks) != hipSuccess ||
-      hipMalloc(&clocks, sizeof(long long) * 2 * (size_t)blocks) != hipSuccess) {
-    rc = fail(HARP_RA_ENOMEM, "probe buffers: hipMalloc failed");
-  } else if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
-    rc = fail(HARP_RA_ELAUNCH, "probe events: hipEventCreate failed");
-  } else {
-    // one warm-up launch (clocks ramp), then the timed one
-    for (int rep = 0; rep < 2 && rc == HARP_RA_OK; ++rep) {
-      (void)hipEventRecord(e0, nullptr);
-      if ((rc = launched(launch_mfma_probe(blocks, iters, seed + (uint32_t)rep, sink, clocks, nullptr), "MFMA probe")))
-        break;
-      (void)hipEventRecord(e1, nullptr);
-      if (hipEventSynchronize(e1) != hipSuccess || hipEventElapsedTime(&best_ms, e0, e1) != hipSuccess)
-        rc = fail(HARP_RA_ELAUNCH, "probe timing failed");
-    }
-    if (rc == HARP_RA_OK &&
-        hipMemcpy(h.data(), clocks, sizeof(long long) * h.size(), hipMemcpyDeviceToHost) != hipSuccess)
-      rc = fail(HARP_RA_ELAUNCH, "probe clock readback failed");
-  }
-  if (rc == HARP_RA_OK) {
-    double shader = 0.0, wall = 0.0;
-    for (int i = 0; i < blocks; ++i) {
-      shader += (double)h[2 * i];
-      wall += (double)h[2 * i + 1];
-    }
-    const double flop = (double)blocks * 4.0 /* waves */ * 4.0 * iters * 32.0 * 32.0 * 16.0 * 2.0;
-    *tflops = (best_ms > 0.f) ? flop / (best_ms * 1e-3) / 1e12 : 0.0;
-    *shader_ghz = (wall > 0.0) ? shader / wall * wall_khz * 1e-6 : 0.0;
-  }
-  if (e0) (void)hipEventDestroy(e0);
-  if (e1) (void)hipEventDestroy(e1);
-  if (sink) (void)hipFree(sink);
-  if (clocks) (void)hipFree(clocks);
-  return rc == HARP_RA_OK ? ok() : rc;
-}
-
 size_t harp_ra_forward_workspace_bytes(int batch, int h_num, int h_len, int sp_size, int kv_chunk_len,
                                        const int32_t* kv_valid_lens) {
   Geometry g;
@@ -323,13 +305,13 @@ int harp_ra_forward(const void* q, const int64_t* q_strides, const void* const* 
   if (ring_rank < 0 || ring_rank >= sp_size)
     return fail(HARP_RA_EINVAL, "ring_rank=%d must be in [0, sp_size=%d)", ring_rank, sp_size);
   if (!std::isfinite(scale) || !(scale > 0.f)) return fail(HARP_RA_EINVAL, "scale must be finite and positive");
-  if ((rc = check_bf16_view(q, q_strides, "q"))) return rc;
+  if ((rc = check_bf16_view(q, q_strides, h_len, "q"))) return rc;
   if (!k_chunks || !v_chunks) return fail(HARP_RA_EINVAL, "k_chunks / v_chunks are NULL");
   for (int c = 0; c < sp_size; ++c) {
-    if ((rc = check_bf16_view(k_chunks[c], kv_strides, "k chunk"))) return rc;
-    if ((rc = check_bf16_view(v_chunks[c], kv_strides, "v chunk"))) return rc;
+    if ((rc = check_bf16_view(k_chunks[c], kv_strides, h_len, "k chunk"))) return rc;
+    if ((rc = check_bf16_view(v_chunks[c], kv_strides, h_len, "v chunk"))) return rc;
   }
-  if ((rc = check_plain_view(out, out_strides, "out"))) return rc;
+  if ((rc = check_out_view(out, out_strides, batch, h_num, t_num, h_len, "out"))) return rc;
   if ((rc = check_extent(kv_chunk_len, kv_strides, "k/v chunk"))) return rc;
   if (!m_i || !l_i) return fail(HARP_RA_EINVAL, "m_i / l_i are NULL");
   if (m_i_dtype != HARP_RA_F32 && m_i_dtype != HARP_RA_BF16) return fail(HARP_RA_EINVAL, "m_i_dtype must be F32 or BF16");
@@ -377,7 +359,7 @@ int harp_ra_delta(const void* grad_out, const int64_t* do_strides, const float* 
                   float* delta, int batch, int h_num, int t_num, int h_len, void* stream) {
   int rc;
   if ((rc = check_dims(batch, h_num, t_num, h_len))) return rc;
-  if ((rc = check_bf16_view(grad_out, do_strides, "grad_out"))) return rc;
+  if ((rc = check_bf16_view(grad_out, do_strides, h_len, "grad_out"))) return rc;
   if ((rc = check_plain_view(out, out_strides, "out"))) return rc;
   if (!delta) return fail(HARP_RA_EINVAL, "delta is NULL");
   DeltaParams p;
@@ -415,18 +397,18 @@ int harp_ra_backward(const void* q, const int64_t* q_strides, void* grad_q, cons
   if (ring_rank < 0 || ring_rank >= sp_size)
     return fail(HARP_RA_EINVAL, "ring_rank=%d must be in [0, sp_size=%d)", ring_rank, sp_size);
   if (!std::isfinite(scale) || !(scale > 0.f)) return fail(HARP_RA_EINVAL, "scale must be finite and positive");
-  if ((rc = check_bf16_view(q, q_strides, "q"))) return rc;
-  if ((rc = check_bf16_view(grad_out, do_strides, "grad_out"))) return rc;
-  if ((rc = check_plain_view(grad_q, dq_strides, "grad_q"))) return rc;
+  if ((rc = check_bf16_view(q, q_strides, h_len, "q"))) return rc;
+  if ((rc = check_bf16_view(grad_out, do_strides, h_len, "grad_out"))) return rc;
+  if ((rc = check_out_view(grad_q, dq_strides, batch, h_num, t_num, h_len, "grad_q"))) return rc;
   if (dq_dtype != HARP_RA_F32 && dq_dtype != HARP_RA_BF16) return fail(HARP_RA_EINVAL, "dq_dtype must be F32 or BF16");
   if (dkv_dtype != HARP_RA_F32 && dkv_dtype != HARP_RA_BF16)
     return fail(HARP_RA_EINVAL, "dkv_dtype must be F32 or BF16");
   if (!k_chunks || !v_chunks || !dk_chunks || !dv_chunks) return fail(HARP_RA_EINVAL, "chunk pointer arrays are NULL");
   for (int c = 0; c < sp_size; ++c) {
-    if ((rc = check_bf16_view(k_chunks[c], kv_strides, "k chunk"))) return rc;
-    if ((rc = check_bf16_view(v_chunks[c], kv_strides, "v chunk"))) return rc;
-    if ((rc = check_plain_view(dk_chunks[c], dkv_strides, "dK chunk"))) return rc;
-    if ((rc = check_plain_view(dv_chunks[c], dkv_strides, "dV chunk"))) return rc;
+    if ((rc = check_bf16_view(k_chunks[c], kv_strides, h_len, "k chunk"))) return rc;
+    if ((rc = check_bf16_view(v_chunks[c], kv_strides, h_len, "v chunk"))) return rc;
+    if ((rc = check_out_view(dk_chunks[c], dkv_strides, batch, h_num, kv_chunk_len, h_len, "dK chunk"))) return rc;
+    if ((rc = check_out_view(dv_chunks[c], dkv_strides, batch, h_num, kv_chunk_len, h_len, "dV chunk"))) return rc;
   }
   if ((rc = check_extent(kv_chunk_len, kv_strides, "k/v chunk"))) return rc;
   if ((rc = check_extent(t_num, q_strides, "q"))) return rc;

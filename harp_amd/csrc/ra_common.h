@@ -43,6 +43,12 @@ __device__ __forceinline__ f32x16 mfma32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// exp2 clamped to [0, 1]: the median against (0, 1) folds into the clamp bit
+// of v_exp_f32, so it costs no instruction.
+__device__ __forceinline__ float exp2_unit(float x) {
+  return __builtin_amdgcn_fmed3f(__builtin_amdgcn_exp2f(x), 0.f, 1.f);
+}
+
 __device__ __forceinline__ f32x16 zero16() {
   f32x16 z;
 #pragma unroll
@@ -55,6 +61,15 @@ __device__ __forceinline__ bf16x8 zero8() {
 #pragma unroll
   for (int i = 0; i < 8; ++i) z[i] = (bf16)0.f;
   return z;
+}
+
+// Lane index computed anew (v_mbcnt) in an asm the compiler cannot merge with
+// an earlier one: an epilogue that derives its lane-dependent indices from it
+// keeps no such value live (or spilled) across the main loop.
+__device__ __forceinline__ int lane_id_fresh() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
 }
 
 // Row of the 32x32 C layout held in accumulator register r by lane-half g.

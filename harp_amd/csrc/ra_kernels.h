@@ -61,9 +61,4 @@ hipError_t launch_delta(const DeltaParams& p, hipStream_t st);
 hipError_t launch_dq(const BwdParams& p, hipStream_t st);
 hipError_t launch_dkdv(const BwdParams& p, hipStream_t st);
 
-// Sustained-MFMA probe (ra_probe.hip): blocks x 256 threads, each wave runs
-// 4 * iters v_mfma_f32_32x32x16_bf16; sink holds blocks * 256 floats and
-// clocks 2 * blocks (shader-clock ticks, constant-rate ticks) per block.
-hipError_t launch_mfma_probe(int blocks, int iters, uint32_t seed, float* sink, long long* clocks, hipStream_t st);
-
 }  // namespace harp_ra

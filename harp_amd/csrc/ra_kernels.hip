@@ -151,53 +151,6 @@ struct DirectLoader {
   }
 };
 
-// Register-staged copy of one 64-row tile, same slot mapping as
-// DirectLoader: fetch() brings each lane's 16-byte slots global -> registers
-// (compiler-visible buffer loads, range-checked like the direct copies);
-// store() writes them with one ds_write_b128 per slot.  The staged slots
-// live in a separate Data object, so several tiles can be in flight with
-// one set of offsets.
-template <class G, int NW>
-struct StagedLoader {
-  static constexpr int kInstTot = G::SLOTS / 64;
-  static constexpr int kInst = (kInstTot + NW - 1) / NW;
-  struct Data {
-    bf16x8 v[kInst];
-  };
-  uint32_t voff[kInst];
-  int wave, lane;
-  __device__ __forceinline__ void init(int64_t row_stride, int D, int wave_, int lane_) {
-    wave = wave_;
-    lane = lane_;
-#pragma unroll
-    for (int k = 0; k < kInst; ++k) {
-      const int inst = wave + k * NW;
-      int r, c;
-      G::slot(inst * 64 + lane, r, c);
-      const bool ok = inst < kInstTot && c < G::NCH && c * 8 < D;
-      voff[k] = ok ? (uint32_t)(r * row_stride * 2 + c * 16) : kOOB;
-    }
-  }
-  __device__ __forceinline__ bool valid(int k) const { return kInstTot % NW == 0 || wave + k * NW < kInstTot; }
-  __device__ __forceinline__ void fetch(Data& d, const bf16* base, uint32_t bytes) const {
-    const uint64_t a = (uint64_t)base;
-    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
-    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(((uint64_t)hi << 32) | lo), (short)0, (int)__builtin_amdgcn_readfirstlane(bytes), 0x00020000);
-#pragma unroll
-    for (int k = 0; k < kInst; ++k)
-      if (valid(k)) d.v[k] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)voff[k], 0, 0));
-  }
-  __device__ __forceinline__ void store_one(const Data& d, bf16* tile, int k) const {
-    if (valid(k)) *(bf16x8*)(tile + ((wave + k * NW) * 64 + lane) * 8) = d.v[k];
-  }
-  __device__ __forceinline__ void store(const Data& d, bf16* tile) const {
-#pragma unroll
-    for (int k = 0; k < kInst; ++k) store_one(d, tile, k);
-  }
-};
-
 // Row fragment T[rb*32 + l32][16*ks + 8*g .. +7] of a PadTile: per-lane base,
 // immediate per (rb, ks).
 template <int DP>
@@ -293,11 +246,6 @@ struct XorLanes {
   }
 };
 
-// Register-class pins (emit no instructions): long-lived MFMA accumulators
-// and block-constant operands stay in AGPRs, so the allocator neither
-// shuttles them between register files inside the loops nor crowds the VGPRs.
-__device__ __forceinline__ void pin_agpr(f32x16& x) { asm volatile("" : "+a"(x)); }
-__device__ __forceinline__ void pin_agpr(bf16x8& x) { asm volatile("" : "+a"(x)); }
 // Settle a value loaded from global memory before the main loop.  The
 // direct-to-LDS loads are invisible to the compiler, but they count in the
 // same hardware vmcnt: a wait the compiler places inside the loop for a
@@ -310,24 +258,12 @@ __device__ __forceinline__ void settle(float& x) { asm volatile("" : "+v"(x)); }
 // Wave issue priority (s_setprio, 0..3) within a tile.  Two waves share a
 // SIMD and the issue arbiter otherwise favours the older one, which then
 // runs a whole phase ahead and idles at the next barrier while its partner
-// finishes alone.  Mode 2 (default): the level falls as a wave moves through
-// the tile, so the wave that lags gets precedence and both reach the barrier
-// together.  Mode 1: level 1 for MFMA phases, 0 for softmax / bookkeeping.
-#ifndef HARP_SETPRIO
-#define HARP_SETPRIO 1
-#endif
-#ifndef HARP_PRIO_MODE
-#define HARP_PRIO_MODE 2
-#endif
-template <int M1, int M2>
-__device__ __forceinline__ void prio_at() {
-  constexpr int lv = HARP_PRIO_MODE == 2 ? M2 : M1;
-  if constexpr (lv >= 0) {
-    if (HARP_SETPRIO) __builtin_amdgcn_s_setprio(lv);
-  }
+// finishes alone.  The level falls as a wave moves through the tile, so the
+// wave that lags gets precedence and both reach the barrier together.
+template <int LEVEL>
+__device__ __forceinline__ void prio() {
+  __builtin_amdgcn_s_setprio(LEVEL);
 }
-__device__ __forceinline__ void prio_mfma() { prio_at<1, -1>(); }
-__device__ __forceinline__ void prio_valu() { prio_at<0, -1>(); }
 
 // Scheduling fence: the compiler may not move any instruction across it.
 __device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
@@ -469,10 +405,7 @@ constexpr int kFwdWaves = 8;
 constexpr int kFwdRows = 32 * kFwdWaves;
 // Keys per tile = 64 * kFwdSub: fewer barriers, pipeline fills and row-max
 // passes per key; the block's LDS holds two such K / V tiles.
-#ifndef HARP_FWD_SUB
-#define HARP_FWD_SUB 2
-#endif
-constexpr int kFwdSub = HARP_FWD_SUB;
+constexpr int kFwdSub = 2;
 // KSTEPS = ceil(D/16) k-steps of the S contraction; DBLK = ceil(D/32) row
 // blocks of O^T (DP = 32*DBLK >= 16*KSTEPS).  Block = kFwdWaves waves x 32 queries;
 // 64*kFwdSub-key tiles (kFwdSub 64-row LDS sub-tiles).
@@ -565,7 +498,7 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
         nv_rs[sb] = rows_rsrc(nxt.v, p.skt, r0, rows);
       }
     }
-    prio_at<1, 3>();
+    prio<3>();
     // S^T (keys x queries), KB 32-key blocks; step i = (ks = i / KB, kb = i % KB)
     f32x16 s[KB];
 #pragma unroll
@@ -592,7 +525,7 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
           if (kb * 32 + c_row(r, g) >= kv_left) s[kb][r] = -INFINITY;
     }
 
-    prio_at<0, 2>();
+    prio<2>();
     // online softmax, lane = query
     float mx = -INFINITY;
 #pragma unroll
@@ -625,13 +558,13 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
           pf[kb * 2 + hf][j] = (bf16)e;
         }
 
-    prio_at<1, 1>();
+    prio<1>();
     // O^T += V^T P^T; step i = (ks2 = i / DBLK, db = i % DBLK), 16 keys per ks2
     pipelined<2 * KB * DBLK, 2>(
         [&](int i) { return vlo.tr_frag(Vs[buf][(i / DBLK) / 4], ((i / DBLK) % 4) * 16, i % DBLK); },
         [&](int i, const bf16x8& a) { o[i % DBLK] = mfma32x32x16(a, pf[i / DBLK], o[i % DBLK]); });
 
-    prio_at<0, 0>();
+    prio<0>();
     buf ^= 1;
     cur = nxt;
   }
@@ -641,17 +574,21 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
   const float shift = (m_max == -INFINITY) ? 1.f : fast_exp2(m_ref - m_max);
   const float inv = (l_tot > 0.f) ? 1.f / l_tot : 0.f;
   l_tot *= shift;
-  if (!q_ok) return;
-  float* orow = p.out + (int64_t)b * p.sob + (int64_t)h * p.soh + (int64_t)qi * p.sot;
+  // lane-dependent indices again, from a fresh lane id (nothing kept live
+  // across the loop for them)
+  const int lane_e = lane_id_fresh(), g_e = lane_e >> 5;
+  const int qi_e = qt * kFwdRows + wave * 32 + (lane_e & 31);
+  if (qi_e >= p.T) return;
+  float* orow = p.out + (int64_t)b * p.sob + (int64_t)h * p.soh + (int64_t)qi_e * p.sot;
 #pragma unroll
   for (int db = 0; db < DBLK; ++db)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int d = db * 32 + c_row(r, g);
+      const int d = db * 32 + c_row(r, g_e);
       if (d < p.D) orow[d] = o[db][r] * inv;
     }
-  if (g == 0) {
-    const int64_t si = ((int64_t)b * p.H + h) * p.T + qi;
+  if (g_e == 0) {
+    const int64_t si = ((int64_t)b * p.H + h) * p.T + qi_e;
     const float m_nat = m_max * kLn2;
     if (p.m_bf16) {
       const bf16 mh = (bf16)m_nat;
@@ -712,16 +649,13 @@ constexpr int kDqRows = 32 * kDqWaves;
 // C(j) = dQ^T += K_j^T dS_j^T.  Order A(0), A(1)|B(0), C(0), A(2)|B(1), C(1),
 // ..., B(last), C(last), where X|Y places Y's VALU instructions between X's
 // MFMAs, so only one block's softmax per interval is exposed.
-#ifndef HARP_DQ_SUB
-#define HARP_DQ_SUB 2
-#endif
-constexpr int kDqSub = HARP_DQ_SUB;
-#ifndef HARP_DQ_PFA
-#define HARP_DQ_PFA 1
-#endif
-constexpr int kDqPfA = HARP_DQ_PFA;  // S^T / dP^T fragments issued this many steps ahead
-// Pad keys need no mask here: their K/V rows load as zero, so their dS has
-// no effect on dQ^T = K^T dS^T.
+constexpr int kDqSub = 2;
+constexpr int kDqPfA = 1;  // S^T / dP^T fragments issued this many steps ahead
+// Pad keys need no mask here: their K / V rows load as zero, so s = 0 and
+// dS^T = -P D, which dQ^T = K^T dS^T multiplies by the zero K row.  P is
+// clamped to [0, 1] (exact for every valid key, whose score never exceeds
+// the row's LSE): unclamped, a pad key's P = exp2(-LSE2) overflows to inf for
+// a row whose LSE is below about -88, and 0 * inf would turn dQ into NaN.
 template <int KSTEPS, int DBLK>
 __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
   constexpr int DP = DBLK * 32;
@@ -829,7 +763,7 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
     auto softmax_rows = [&](int j, int r0, int nr) {
 #pragma unroll
       for (int r = r0; r < r0 + nr; ++r) {
-        const float pv = fast_exp2(__builtin_fmaf(s[j & 1][r], c2, -lse2_s));
+        const float pv = exp2_unit(__builtin_fmaf(s[j & 1][r], c2, -lse2_s));
         dsf[j & 1][r >> 3][r & 7] = (bf16)(pv * (dp[j & 1][r] - dlt_s));
       }
     };
@@ -869,35 +803,39 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
           [&](int i) { return klo.tr_frag_lean(K, (j & 1) * 32 + (i / DBLK) * 16, i % DBLK); },
           [&](int i, const bf16x8& a) { dq[i % DBLK] = mfma32x32x16(a, dsf[j & 1][i / DBLK], dq[i % DBLK]); });
     };
-    prio_at<1, 3>();
+    prio<3>();
     phase_a(Int<0>{}, Int<-1>{});
     phase_a(Int<1>{}, Int<0>{});
     phase_c(Int<0>{});
     if constexpr (KB > 2) {
-      prio_at<-1, 2>();
+      prio<2>();
       phase_a(Int<2>{}, Int<1>{});
       phase_c(Int<1>{});
-      prio_at<-1, 1>();
+      prio<1>();
       phase_a(Int<3>{}, Int<2>{});
       phase_c(Int<2>{});
     }
-    prio_at<0, 0>();
+    // s_setprio also fences the scheduler: the repeated level-0 calls keep the
+    // last block's softmax and its dQ product as separate scheduling regions
+    prio<0>();
     softmax_rows(KB - 1, 0, 16);
-    prio_at<1, 0>();
+    prio<0>();
     phase_c(Int<KB - 1>{});
-    prio_at<0, 0>();
+    prio<0>();
 
     buf ^= 1;
     cur = nxt;
   }
 
-  if (!q_ok) return;
-  char* drow = (char*)p.dq + (((int64_t)b * p.sdqb + (int64_t)h * p.sdqh + (int64_t)qi * p.sdqt) << (p.dq_f32 ? 2 : 1));
+  const int lane_e = lane_id_fresh(), g_e = lane_e >> 5;  // as in the forward's epilogue
+  const int qi_e = qt * kDqRows + wave * 32 + (lane_e & 31);
+  if (qi_e >= p.T) return;
+  char* drow = (char*)p.dq + (((int64_t)b * p.sdqb + (int64_t)h * p.sdqh + (int64_t)qi_e * p.sdqt) << (p.dq_f32 ? 2 : 1));
 #pragma unroll
   for (int db = 0; db < DBLK; ++db)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int d = db * 32 + c_row(r, g);
+      const int d = db * 32 + c_row(r, g_e);
       if (d < p.D) {
         const float v = dq[db][r] * p.scale;
         if (p.dq_f32) ((float*)drow)[d] = v;
@@ -923,6 +861,8 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
 // LDS read throughput of one.  Each Q / dO tile in LDS serves 256 keys.
 // Pad keys (past the chunk's valid length) are written as zero at the end
 // instead of being masked per tile: a key's P / dS only reach its own dK / dV.
+// P is clamped to [0, 1] as in the dQ kernel, so even a pad key's values stay
+// finite.
 constexpr int kDkWaves = kDkdvBlockKeys / 32;
 template <int KSTEPS, int DBLK>
 __global__ __launch_bounds__(64 * kDkWaves, 1) void dkdv_kernel(BwdParams p) {
@@ -1057,8 +997,8 @@ __global__ __launch_bounds__(64 * kDkWaves, 1) void dkdv_kernel(BwdParams p) {
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb) {
         const float2 st = stats_lane(buf, qb);
-        if (qb == 0) prio_at<1, 3>();
-        else prio_at<1, 1>();
+        if (qb == 0) prio<3>();
+        else prio<1>();
         f32x16 s = zero16(), dp = zero16();
         pipelined<KSTEPS, 1>(
             [&](int ks) { return Frag2{lo.row_frag_lean(Q, qb, ks), lo.row_frag_lean(Gd, qb, ks)}; },
@@ -1076,17 +1016,17 @@ __global__ __launch_bounds__(64 * kDkWaves, 1) void dkdv_kernel(BwdParams p) {
               }
               dp = mfma32x32x16(f.b, v, dp);
             });
-        if (qb == 0) prio_at<0, 3>();
-        else prio_at<0, 1>();
+        if (qb == 0) prio<3>();
+        else prio<1>();
         bf16x8 pf[2], dsf[2];
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const float pv = fast_exp2(__builtin_fmaf(s[r], c2, -row_bcast(st.x, r)));
+          const float pv = exp2_unit(__builtin_fmaf(s[r], c2, -row_bcast(st.x, r)));
           pf[r >> 3][r & 7] = (bf16)pv;
           dsf[r >> 3][r & 7] = (bf16)(pv * (dp[r] - row_bcast(st.y, r)));
         }
-        if (qb == 0) prio_at<1, 2>();
-        else prio_at<1, 0>();
+        if (qb == 0) prio<2>();
+        else prio<0>();
         // dV += P^T dO ; dK += dS^T Q (M = keys, N = d, K = the 32 queries of
         // this half); step s2 = (h2 = s2 / DBLK, db = s2 % DBLK)
         pipelined<2 * DBLK, 1>(
@@ -1100,7 +1040,7 @@ __global__ __launch_bounds__(64 * kDkWaves, 1) void dkdv_kernel(BwdParams p) {
               dk[db] = mfma32x32x16(dsf[h2], f.b, dk[db]);
             });
       }
-      prio_at<0, 0>();
+      prio<0>();
       if (t + 1 < n_tiles) store_stats(buf ^ 1);
       buf ^= 1;
     }
@@ -1109,13 +1049,14 @@ __global__ __launch_bounds__(64 * kDkWaves, 1) void dkdv_kernel(BwdParams p) {
   // store: C layout row = key key0 + c_row(r,g), col = d = db*32 + l32;
   // keys past the valid length (pads) get zero
   const int64_t base = (int64_t)b * p.sdkb + (int64_t)h * p.sdkh;
+  const int lane_e = lane_id_fresh(), g_e = lane_e >> 5;  // as in the forward's epilogue
 #pragma unroll
   for (int db = 0; db < DBLK; ++db) {
-    const int d = db * 32 + l32;
+    const int d = db * 32 + (lane_e & 31);
     if (d >= p.D) continue;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int kk = key0 + c_row(r, g);
+      const int kk = key0 + c_row(r, g_e);
       if (kk >= p.ct_rows[c]) continue;
       const int64_t e = base + (int64_t)kk * p.sdkt + d;
       const bool valid = kk < len;

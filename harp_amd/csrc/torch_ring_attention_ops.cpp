@@ -4,23 +4,32 @@
 //
 // Registers namespace ring_attention_ops with the reference's two schemas
 // (gemm/ring_attention/torch_ring_attention_ops.cpp:260-263) extended only by
-// trailing defaulted arguments, so every existing positional call is valid:
+// trailing defaulted arguments, so every existing positional call parses:
 //   ring_attention_forward(q, k, v, out!, m_i!, l_i!, sp_size, scale,
-//                          ring_rank=0, kv_lens=None)
+//                          ring_rank=0, kv_lens=None, kv_chunk_len=0)
 //   ring_attention_backward(q, grad_q!, k, dK!, v, dV!, grad_out, m_i, l_i, D,
-//                           sp_size, scale, ring_rank=0, kv_lens=None)
+//                           sp_size, scale, ring_rank=0, kv_lens=None,
+//                           kv_chunk_len=0)
 // plus ring_attention_delta(grad_out, out) -> D, the rowsum(dO*O) preprocess
 // of src/models/z_image/module/attn.py:41 as one kernel.
 //
 // Implementations are registered for the CUDA dispatch key (PyTorch-ROCm
 // tensors on a HIP device carry it) and call libharp_ra.so through its C ABI
-// on the current HIP stream; they never synchronise.  The CPU key raises:
-// this build has no CPU path.
+// on the current HIP stream; they never synchronise.  The CPU key validates
+// the call's shapes, then raises: this build has no CPU path.
 //
 // Single-GPU ring semantics: k and v hold every KV chunk of the ring,
-// concatenated along dim 2 (sp_size chunks of k.size(2) / sp_size rows);
-// dK / dV have k's shape and receive the local queries' contribution to each
-// chunk.  kv_lens optionally gives the valid (unmasked) rows of each chunk.
+// concatenated along dim 2; dK / dV have k's shape and receive the local
+// queries' contribution to each chunk.  kv_lens optionally gives the valid
+// (unmasked) rows of each chunk.  The chunk length is
+//   * kv_chunk_len when it is > 0 (k.size(2) must be sp_size * kv_chunk_len);
+//   * else, when kv_lens is given, k.size(2) / sp_size;
+//   * else (the reference's positional call) k.size(2) when sp_size == 1, or
+//     q.size(2) when k.size(2) == sp_size * q.size(2).
+// Any other reference-shaped call is rejected.  In particular HARP's own call
+// (attn.py:29: k / v hold only the local chunk, the other sp_size - 1 chunks
+// live on peer ranks, ring_attn.cpp:2424-2426) cannot be served on one GPU
+// and raises instead of silently attending over the local keys only.
 #include <ATen/ATen.h>
 #include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
@@ -34,7 +43,14 @@
 
 namespace {
 
-std::array<int64_t, 4> strides4(const at::Tensor& t) { return {t.stride(0), t.stride(1), t.stride(2), t.stride(3)}; }
+// Element strides of a [B, H, T, D] view.  A size-1 dim may carry any stride
+// in torch; the kernels derive buffer ranges from the T stride, so a single
+// row reports a T stride of at least one row.
+std::array<int64_t, 4> strides4(const at::Tensor& t) {
+  std::array<int64_t, 4> s = {t.stride(0), t.stride(1), t.stride(2), t.stride(3)};
+  if (t.size(2) == 1 && s[2] < t.size(3)) s[2] = (t.size(3) + 7) / 8 * 8;
+  return s;
+}
 
 void check_status(int rc, const char* op) {
   TORCH_CHECK(rc == HARP_RA_OK, "ring_attention_ops.", op, ": ", harp_ra_last_error(), " (status ", rc, ")");
@@ -69,19 +85,43 @@ struct Chunks {
   int chunk_len = 0;
 };
 
-Chunks split_chunks(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, int64_t sp_size,
-                    at::OptionalIntArrayRef kv_lens) {
-  TORCH_CHECK(sp_size >= 1 && sp_size <= HARP_RA_MAX_CHUNKS, "sp_size must be in [1, ", HARP_RA_MAX_CHUNKS,
-              "], got ", sp_size);
+Chunks split_chunks(const char* op, const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, int64_t sp_size,
+                    at::OptionalIntArrayRef kv_lens, int64_t kv_chunk_len) {
+  TORCH_CHECK(sp_size >= 1 && sp_size <= HARP_RA_MAX_CHUNKS, "ring_attention_ops.", op, ": sp_size must be in [1, ",
+              HARP_RA_MAX_CHUNKS, "], got ", sp_size);
   TORCH_CHECK(k.sizes() == v.sizes(), "k and v must have the same shape");
   TORCH_CHECK(k.size(0) == q.size(0) && k.size(1) == q.size(1) && k.size(3) == q.size(3),
               "k/v must match q on B, H and D");
   TORCH_CHECK(k.strides() == v.strides(), "k and v must have the same strides");
-  TORCH_CHECK(k.size(2) % sp_size == 0, "on one GPU k/v hold all sp_size KV chunks along dim 2: k.size(2)=",
-              k.size(2), " is not a multiple of sp_size=", sp_size);
+  TORCH_CHECK(kv_chunk_len >= 0, "ring_attention_ops.", op, ": kv_chunk_len must be >= 0, got ", kv_chunk_len);
+  const int64_t rows = k.size(2);
+  int64_t chunk = 0;
+  if (kv_chunk_len > 0) {
+    TORCH_CHECK(rows == sp_size * kv_chunk_len, "ring_attention_ops.", op, ": k.size(2)=", rows,
+                " must equal sp_size * kv_chunk_len = ", sp_size, " * ", kv_chunk_len);
+    chunk = kv_chunk_len;
+  } else if (kv_lens.has_value()) {
+    TORCH_CHECK(rows % sp_size == 0, "ring_attention_ops.", op, ": with kv_lens, k/v hold all sp_size KV chunks along ",
+                "dim 2: k.size(2)=", rows, " is not a multiple of sp_size=", sp_size);
+    chunk = rows / sp_size;
+  } else if (sp_size == 1) {
+    chunk = rows;
+  } else if (rows == sp_size * q.size(2)) {
+    chunk = q.size(2);
+  } else if (rows == q.size(2)) {
+    TORCH_CHECK(false, "ring_attention_ops.", op, ": k/v hold only the local chunk (k.size(2) == q.size(2) == ", rows,
+                ") with sp_size=", sp_size,
+                " > 1: the other ranks' chunks would come from peers, which one GPU does not have. Pass all ",
+                "sp_size chunks concatenated along dim 2 (k.size(2) == sp_size * q.size(2)), or give kv_chunk_len ",
+                "(INTEGRATION.md section 2)");
+  } else {
+    TORCH_CHECK(false, "ring_attention_ops.", op, ": k.size(2)=", rows, " does not match sp_size=", sp_size,
+                " chunks of q.size(2)=", q.size(2), " rows; pass kv_chunk_len (k.size(2) == sp_size * kv_chunk_len) ",
+                "for another chunk length");
+  }
   Chunks c;
-  c.chunk_len = static_cast<int>(k.size(2) / sp_size);
-  const int64_t step = c.chunk_len * k.stride(2) * k.element_size();
+  c.chunk_len = static_cast<int>(chunk);
+  const int64_t step = chunk * k.stride(2) * k.element_size();
   for (int64_t i = 0; i < sp_size; ++i) {
     c.k.push_back(static_cast<const char*>(k.data_ptr()) + i * step);
     c.v.push_back(static_cast<const char*>(v.data_ptr()) + i * step);
@@ -105,7 +145,8 @@ void* ws_ptr(const at::Tensor& ws) { return ws.numel() ? ws.data_ptr() : nullptr
 std::tuple<at::Tensor, at::Tensor, at::Tensor> forward_hip(const at::Tensor& q, const at::Tensor& k,
                                                            const at::Tensor& v, at::Tensor out, at::Tensor m_i,
                                                            at::Tensor l_i, int64_t sp_size, double scale,
-                                                           int64_t ring_rank, at::OptionalIntArrayRef kv_lens) {
+                                                           int64_t ring_rank, at::OptionalIntArrayRef kv_lens,
+                                                           int64_t kv_chunk_len) {
   check_bhtd(q, "q");
   check_bhtd(k, "k");
   check_bhtd(v, "v");
@@ -121,7 +162,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> forward_hip(const at::Tensor& q, 
   check_stats(l_i, q, "l_i");
   TORCH_CHECK(l_i.scalar_type() == at::kFloat, "l_i must be float32");
   const int m_code = dtype_code(m_i, "m_i");
-  Chunks ch = split_chunks(q, k, v, sp_size, kv_lens);
+  Chunks ch = split_chunks("ring_attention_forward", q, k, v, sp_size, kv_lens, kv_chunk_len);
   const c10::DeviceGuard guard(q.device());
   const int B = q.size(0), H = q.size(1), T = q.size(2), D = q.size(3);
   const int32_t* lens = ch.lens.empty() ? nullptr : ch.lens.data();
@@ -143,7 +184,8 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> backward_hip(const at::Tensor& q,
                                                             at::Tensor dV, const at::Tensor& grad_out,
                                                             const at::Tensor& m_i, const at::Tensor& l_i,
                                                             const at::Tensor& D, int64_t sp_size, double scale,
-                                                            int64_t ring_rank, at::OptionalIntArrayRef kv_lens) {
+                                                            int64_t ring_rank, at::OptionalIntArrayRef kv_lens,
+                                                            int64_t kv_chunk_len) {
   const std::array<const at::Tensor*, 7> ops4 = {&q, &grad_q, &k, &dK, &v, &dV, &grad_out};
   for (const at::Tensor* t : ops4) check_bhtd(*t, "gradient operand");
   const std::array<const at::Tensor*, 9> dev_ops = {&grad_q, &k, &dK, &v, &dV, &grad_out, &m_i, &l_i, &D};
@@ -163,7 +205,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> backward_hip(const at::Tensor& q,
   const int m_code = dtype_code(m_i, "m_i");
   const int dq_code = dtype_code(grad_q, "grad_q");
   const int dkv_code = dtype_code(dK, "dK");
-  Chunks ch = split_chunks(q, k, v, sp_size, kv_lens);
+  Chunks ch = split_chunks("ring_attention_backward", q, k, v, sp_size, kv_lens, kv_chunk_len);
   const int64_t dstep = ch.chunk_len * dK.stride(2) * dK.element_size();
   for (int64_t i = 0; i < sp_size; ++i) {
     ch.dk.push_back(static_cast<char*>(dK.data_ptr()) + i * dstep);
@@ -208,16 +250,27 @@ at::Tensor delta_hip(const at::Tensor& grad_out, const at::Tensor& out) {
               ": this MI355X build runs on HIP devices only; move the tensors to the GPU (there is no CPU path)");
 }
 
-std::tuple<at::Tensor, at::Tensor, at::Tensor> forward_cpu(const at::Tensor&, const at::Tensor&, const at::Tensor&,
-                                                           at::Tensor, at::Tensor, at::Tensor, int64_t, double,
-                                                           int64_t, at::OptionalIntArrayRef) {
+// The CPU key runs the shape contract first, so a call that could never run
+// on the GPU either reports that, then refuses the CPU tensors.
+std::tuple<at::Tensor, at::Tensor, at::Tensor> forward_cpu(const at::Tensor& q, const at::Tensor& k,
+                                                           const at::Tensor& v, at::Tensor, at::Tensor, at::Tensor,
+                                                           int64_t sp_size, double, int64_t,
+                                                           at::OptionalIntArrayRef kv_lens, int64_t kv_chunk_len) {
+  check_bhtd(q, "q");
+  check_bhtd(k, "k");
+  check_bhtd(v, "v");
+  (void)split_chunks("ring_attention_forward", q, k, v, sp_size, kv_lens, kv_chunk_len);
   no_cpu_path("ring_attention_forward");
 }
-std::tuple<at::Tensor, at::Tensor, at::Tensor> backward_cpu(const at::Tensor&, at::Tensor, const at::Tensor&,
-                                                            at::Tensor, const at::Tensor&, at::Tensor,
+std::tuple<at::Tensor, at::Tensor, at::Tensor> backward_cpu(const at::Tensor& q, at::Tensor, const at::Tensor& k,
+                                                            at::Tensor, const at::Tensor& v, at::Tensor,
                                                             const at::Tensor&, const at::Tensor&, const at::Tensor&,
-                                                            const at::Tensor&, int64_t, double, int64_t,
-                                                            at::OptionalIntArrayRef) {
+                                                            const at::Tensor&, int64_t sp_size, double, int64_t,
+                                                            at::OptionalIntArrayRef kv_lens, int64_t kv_chunk_len) {
+  check_bhtd(q, "q");
+  check_bhtd(k, "k");
+  check_bhtd(v, "v");
+  (void)split_chunks("ring_attention_backward", q, k, v, sp_size, kv_lens, kv_chunk_len);
   no_cpu_path("ring_attention_backward");
 }
 at::Tensor delta_cpu(const at::Tensor&, const at::Tensor&) { no_cpu_path("ring_attention_delta"); }
@@ -227,11 +280,12 @@ at::Tensor delta_cpu(const at::Tensor&, const at::Tensor&) { no_cpu_path("ring_a
 TORCH_LIBRARY(ring_attention_ops, m) {
   m.def(
       "ring_attention_forward(Tensor q, Tensor k, Tensor v, Tensor(a!) out, Tensor(b!) m_i, Tensor(c!) l_i, "
-      "int sp_size, float scale, int ring_rank=0, int[]? kv_lens=None) -> (Tensor(a!), Tensor(b!), Tensor(c!))");
+      "int sp_size, float scale, int ring_rank=0, int[]? kv_lens=None, int kv_chunk_len=0) -> (Tensor(a!), Tensor(b!), "
+      "Tensor(c!))");
   m.def(
       "ring_attention_backward(Tensor q, Tensor(a!) grad_q, Tensor k, Tensor(b!) dK, Tensor v, Tensor(c!) dV, "
       "Tensor grad_out, Tensor m_i, Tensor l_i, Tensor D, int sp_size, float scale, int ring_rank=0, "
-      "int[]? kv_lens=None) -> (Tensor(a!), Tensor(b!), Tensor(c!))");
+      "int[]? kv_lens=None, int kv_chunk_len=0) -> (Tensor(a!), Tensor(b!), Tensor(c!))");
   m.def("ring_attention_delta(Tensor grad_out, Tensor out) -> Tensor");
 }
 

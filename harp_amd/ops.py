@@ -11,7 +11,8 @@
   chunks of the ring need not be contiguous.
 
 Single-GPU ring semantics: ``k``/``v`` carry all ``sp_size`` chunks of the
-ring concatenated along dim 2; chunk ``c`` is visited at step
+ring concatenated along dim 2 (``k.size(2) / sp_size`` rows each, passed to
+the operators as ``kv_chunk_len``); chunk ``c`` is visited at step
 ``(c - ring_rank) % sp_size`` (ring_attn.cpp:2497).
 """
 
@@ -38,6 +39,10 @@ class RingAttention(torch.autograd.Function):
         ctx.sp_size = sp_size
         ctx.ring_rank = ring_rank
         ctx.kv_lens = kv_lens
+        if local_k.size(2) % sp_size:
+            raise ValueError(f"k/v hold all sp_size={sp_size} chunks along dim 2: k.size(2)={local_k.size(2)} "
+                             "is not a multiple of sp_size")
+        ctx.chunk_len = local_k.size(2) // sp_size
         scale = 1.0 / math.sqrt(local_q.size(-1))  # attn.py:20
         ctx.scale = scale
         mm_type = local_q.dtype
@@ -47,7 +52,8 @@ class RingAttention(torch.autograd.Function):
         out = torch.empty_like(local_q, dtype=torch.float32)
         m_i = torch.full((B, H, T, 1), float("-inf"), device=local_q.device, dtype=torch.bfloat16)
         l_i = torch.empty((B, H, T, 1), device=local_q.device, dtype=torch.float32)
-        _ops().ring_attention_forward(local_q, local_k, local_v, out, m_i, l_i, sp_size, scale, ring_rank, kv_lens)
+        _ops().ring_attention_forward(local_q, local_k, local_v, out, m_i, l_i, sp_size, scale, ring_rank, kv_lens,
+                                      ctx.chunk_len)
         ctx.save_for_backward(local_q, local_k, local_v, out, m_i, l_i)
         return out.to(mm_type)
 
@@ -61,7 +67,7 @@ class RingAttention(torch.autograd.Function):
         grad_v = torch.empty_like(local_v, dtype=torch.bfloat16)
         _ops().ring_attention_backward(
             local_q, grad_q, local_k, grad_k, local_v, grad_v, grad_out, m_i, l_i, D,
-            ctx.sp_size, ctx.scale, ctx.ring_rank, ctx.kv_lens,
+            ctx.sp_size, ctx.scale, ctx.ring_rank, ctx.kv_lens, ctx.chunk_len,
         )
         return grad_q, grad_k, grad_v, None, None, None
 

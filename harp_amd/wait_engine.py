@@ -54,6 +54,7 @@ class WaitEngine:
     def __init__(self) -> None:
         self.task_queue: "queue.Queue" = queue.Queue()
         self.stop_event = threading.Event()
+        self._submit_lock = threading.Lock()  # orders submit() against shutdown()
         core = os.environ.get("HARP_WAIT_ENGINE_CORE")
         self.core_id = int(core) if core not in (None, "") else None
         self.worker_thread = threading.Thread(target=self._run, daemon=True, name="harp-wait-engine")
@@ -71,10 +72,14 @@ class WaitEngine:
     def _wait_on(req: Any) -> None:
         if req is None:
             return
-        if hasattr(req, "synchronize") and not hasattr(req, "wait"):
-            req.synchronize()  # torch.cuda.Event
+        if _is_device_event(req):
+            # a device event is waited on by the host: Event.wait() would only
+            # make the worker thread's current stream wait and return at once
+            req.synchronize()
         elif hasattr(req, "wait"):
-            req.wait()
+            req.wait()  # torch.distributed work handle (or any object with wait())
+        elif hasattr(req, "synchronize"):
+            req.synchronize()
         else:
             raise TypeError(f"cannot wait on {type(req).__name__}")
 
@@ -96,12 +101,34 @@ class WaitEngine:
     def submit(self, req: Any) -> CommWork:
         task = CommWork()
         task.work_handle = req
-        self.task_queue.put((req, task))
+        with self._submit_lock:
+            if self.stop_event.is_set():
+                raise RuntimeError("wait engine is shut down")
+            self.task_queue.put((req, task))
         return task
 
     def shutdown(self) -> None:
-        self.stop_event.set()
+        """Stop the worker.  Requests still queued are not waited on: their
+        CommWork is completed with an error, so no caller blocks forever."""
+        with self._submit_lock:
+            self.stop_event.set()
         self.worker_thread.join()
+        while True:
+            try:
+                _, task = self.task_queue.get_nowait()
+            except queue.Empty:
+                break
+            task.error = RuntimeError("wait engine shut down before the request was waited on")
+            task.mark_done()
+            self.task_queue.task_done()
         with WaitEngine._lock:
             if WaitEngine._instance is self:
                 WaitEngine._instance = None
+
+
+def _is_device_event(req: Any) -> bool:
+    try:
+        import torch
+    except ImportError:  # pragma: no cover - torch is a dependency of the package
+        return False
+    return isinstance(req, torch.cuda.Event)

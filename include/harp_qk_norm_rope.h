@@ -66,7 +66,11 @@ HARP_QK_API int harp_qk_rmsnorm_forward(const void* x, const int64_t* x_strides,
  * RMSNorm backward: dx from dy, the forward input x and the saved rms;
  * grad_weight (bf16 or fp32 per grad_weight_dtype, may be NULL) = sum over
  * all rows of dy * x / rms.  workspace: harp_qk_backward_workspace_bytes()
- * bytes of device memory, or NULL for a library-owned one.
+ * bytes of device memory, or NULL for a library-owned one.  The library keeps
+ * one such buffer per (device, stream), grown with hipMalloc when a call needs
+ * more (after the stream drains): calls on different streams never share it,
+ * but a NULL-workspace call allocates and so cannot be captured into a HIP
+ * graph; callers that capture pass a workspace.
  * Replaces: rmsnorm_backward_out(Tensor input, Tensor grad_output, Tensor
  *   weight, Tensor rms, Tensor(a!) grad_input, Tensor(b!) grad_weight) —
  *   async_rt/csrc/rms_norm.cc:484-522 (kernel :107-240), schema

@@ -145,18 +145,6 @@ enum {
 HARP_RA_API int harp_ra_timing_enable(int enable);
 HARP_RA_API int harp_ra_timing_read(double* ms, int* launches, int n_kinds);
 
-/*
- * Device probe (no reference counterpart; a measurement aid): the sustained
- * dense bf16 MFMA rate of the current device, in TFLOP/s, and the average
- * shader clock in GHz while it ran.  Every wave streams
- * v_mfma_f32_32x32x16_bf16 from registers on pseudo-random bf16 operands
- * (from seed), 32 waves per CU, 4 * iters MFMAs per wave (4096 is ~3 ms on
- * an MI355X).  The rate bounds any MFMA-bound kernel under the board's power
- * limit.  Synchronous on the null stream; allocates and frees its own small
- * buffers.
- */
-HARP_RA_API int harp_ra_probe_mfma_rate(int iters, uint32_t seed, double* tflops, double* shader_ghz);
-
 /* Library version string. No reference counterpart. */
 HARP_RA_API const char* harp_ra_version(void);
 

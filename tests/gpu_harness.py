@@ -63,7 +63,7 @@ def run_hip(
     else:
         harp_amd.load_ops()
         torch.ops.ring_attention_ops.ring_attention_forward(
-            qd, kd[0], vd[0], out, m_i, l_i, n, scale, ring_rank, None if kv_lens is None else list(kv_lens))
+            qd, kd[0], vd[0], out, m_i, l_i, n, scale, ring_rank, None if kv_lens is None else list(kv_lens), tc)
     res = {"o": out, "m": m_i, "l": l_i}
     if backward:
         dod = token_major_dev(do) if do_layout == "token" else head_major_dev(do)
@@ -86,7 +86,7 @@ def run_hip(
             dv_all = torch.full((B, n * tc, H, D), float("nan"), device=dev, dtype=grad_dtype).transpose(1, 2)
             torch.ops.ring_attention_ops.ring_attention_backward(
                 qd, dq, kd[0], dk_all, vd[0], dv_all, dod, m_i, l_i, delta, n, scale, ring_rank,
-                None if kv_lens is None else list(kv_lens))
+                None if kv_lens is None else list(kv_lens), tc)
         res.update(delta=delta, dq=dq, dk=dk_all, dv=dv_all)
     torch.cuda.synchronize()
     cpu = {k: v.cpu() for k, v in res.items()}

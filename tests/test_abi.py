@@ -77,6 +77,13 @@ def _fwd_call(**over):
         (dict(mdt=7), _lib.HARP_RA_EINVAL, "m_i_dtype"),
         (dict(scale=float("nan")), _lib.HARP_RA_EINVAL, "scale"),
         (dict(scale=-0.125), _lib.HARP_RA_EINVAL, "positive"),
+        # a row stride of 0 (an expanded view) or below D would cut every row short
+        (dict(ks=_lib.i64_array([8 * 64 * 128, 64, 0, 1])), _lib.HARP_RA_EINVAL, "row stride"),
+        (dict(qs=_lib.i64_array([8 * 64 * 128, 64, 56, 1])), _lib.HARP_RA_EINVAL, "row stride"),
+        # outputs whose strides alias elements are refused (stores would race)
+        (dict(os=_lib.i64_array([8 * 64 * 128, 64, 0, 1])), _lib.HARP_RA_EINVAL, "overlap"),
+        (dict(os=_lib.i64_array([8 * 64 * 128, 0, 8 * 64, 1])), _lib.HARP_RA_EINVAL, "overlap"),
+        (dict(os=_lib.i64_array([8 * 64 * 128, 32, 8 * 64, 1])), _lib.HARP_RA_EINVAL, "overlap"),
     ],
 )
 def test_forward_rejects_bad_arguments_before_any_device_call(over, code, msg):
@@ -111,8 +118,9 @@ def test_operator_library_registers_reference_schemas():
     assert f.startswith("ring_attention_ops::" + REF_FWD_SCHEMA)
     assert b.startswith("ring_attention_ops::" + REF_BWD_SCHEMA)
     # reference positional calls stay valid: only defaulted trailing args were added
-    assert f.endswith("int ring_rank=0, int[]? kv_lens=None) -> (Tensor(a!), Tensor(b!), Tensor(c!))")
-    assert b.endswith("int ring_rank=0, int[]? kv_lens=None) -> (Tensor(a!), Tensor(b!), Tensor(c!))")
+    tail = "int ring_rank=0, int[]? kv_lens=None, int kv_chunk_len=0) -> (Tensor(a!), Tensor(b!), Tensor(c!))"
+    assert f.endswith(tail)
+    assert b.endswith(tail)
 
 
 def test_cpu_tensors_raise_instead_of_falling_back():
@@ -136,3 +144,82 @@ def test_product_package_never_imports_the_oracle():
             if fn.endswith((".py", ".cpp", ".hip", ".h")):
                 text = open(os.path.join(dirpath, fn)).read()
                 assert "oracle" not in text.replace("oracle/", "").lower() or fn == "build.py", fn
+
+
+def _bwd_call(**over):
+    lib = harp_amd.load_abi()
+    st = _lib.i64_array([8 * 64 * 128, 64, 8 * 64, 1])
+    fake = 1 << 20  # never dereferenced: validation fails first
+    a = dict(q=fake, qs=st, dq=fake, dqs=st, dqt=_lib.HARP_RA_BF16, kc=_lib.ptr_array([fake]),
+             vc=_lib.ptr_array([fake]), ks=st, dkc=_lib.ptr_array([fake]), dvc=_lib.ptr_array([fake]), dks=st,
+             dkt=_lib.HARP_RA_BF16, tc=128, lens=None, do=fake, dos=st, m=fake, mdt=_lib.HARP_RA_BF16, l=fake,
+             d=fake, B=1, H=8, T=128, D=64, sp=1, rank=0, scale=0.125, ws=None, wsb=0, stream=None)
+    a.update(over)
+    return lib.harp_ra_backward(a["q"], a["qs"], a["dq"], a["dqs"], a["dqt"], a["kc"], a["vc"], a["ks"], a["dkc"],
+                                a["dvc"], a["dks"], a["dkt"], a["tc"], a["lens"], a["do"], a["dos"], a["m"],
+                                a["mdt"], a["l"], a["d"], a["B"], a["H"], a["T"], a["D"], a["sp"], a["rank"],
+                                a["scale"], a["ws"], a["wsb"], a["stream"])
+
+
+@pytest.mark.parametrize(
+    "over,msg",
+    [
+        (dict(dos=_lib.i64_array([8 * 64 * 128, 64, 0, 1])), "grad_out row stride"),
+        (dict(ks=_lib.i64_array([0, 0, 0, 1])), "k chunk row stride"),
+        (dict(dqs=_lib.i64_array([8 * 64 * 128, 64, 0, 1])), "grad_q strides make elements overlap"),
+        (dict(dks=_lib.i64_array([8 * 64 * 128, 0, 8 * 64, 1])), "dK chunk strides make elements overlap"),
+    ],
+)
+def test_backward_rejects_degenerate_strides(over, msg):
+    assert _bwd_call(**over) == _lib.HARP_RA_EINVAL
+    assert msg in _lib.last_error()
+
+
+def _cpu_qkv(T=16, Tk=16, H=2, D=64):
+    q = torch.zeros(1, H, T, D, dtype=torch.bfloat16)
+    k = torch.zeros(1, H, Tk, D, dtype=torch.bfloat16)
+    out = torch.zeros(1, H, T, D)
+    m = torch.zeros(1, H, T, 1, dtype=torch.bfloat16)
+    l = torch.zeros(1, H, T, 1)
+    return q, k, out, m, l
+
+
+def test_reference_local_only_call_is_rejected():
+    """HARP's own call (attn.py:29): k / v hold only the local chunk while
+    sp_size > 1.  One GPU has no peers to take the other chunks from, so the
+    operator refuses it rather than attending over the local keys only."""
+    harp_amd.load_ops()
+    ops = torch.ops.ring_attention_ops
+    q, k, out, m, l = _cpu_qkv(T=16, Tk=16)
+    with pytest.raises(RuntimeError, match="hold only the local chunk"):
+        ops.ring_attention_forward(q, k, k, out, m, l, 4, 0.125)
+    with pytest.raises(RuntimeError, match="hold only the local chunk"):
+        ops.ring_attention_backward(q, q, k, k, k, k, q, l, l, l, 4, 0.125)
+
+
+@pytest.mark.parametrize(
+    "Tk,sp,lens,chunk,expect",
+    [
+        (64, 4, None, 0, "no CPU path"),        # all sp_size chunks of q's length: accepted
+        (40, 1, None, 0, "no CPU path"),        # sp_size 1: k is the one chunk, any length
+        (48, 4, None, 0, "does not match"),     # neither pattern: refused without kv_chunk_len
+        (48, 4, None, 12, "no CPU path"),       # explicit chunk length: accepted
+        (48, 4, None, 16, "must equal sp_size"),
+        (48, 4, [12, 12, 10, 0], 0, "no CPU path"),  # kv_lens opts in to k.size(2) / sp_size
+        (50, 4, [12, 12, 10, 0], 0, "not a multiple"),
+    ],
+)
+def test_chunk_layout_contract(Tk, sp, lens, chunk, expect):
+    """Which k / v shapes the operator accepts; the CPU key checks the layout
+    before it refuses CPU tensors, so these run without a GPU."""
+    harp_amd.load_ops()
+    q, k, out, m, l = _cpu_qkv(T=16, Tk=Tk)
+    with pytest.raises(RuntimeError, match=expect):
+        torch.ops.ring_attention_ops.ring_attention_forward(q, k, k, out, m, l, sp, 0.125, 0, lens, chunk)
+    with pytest.raises(RuntimeError, match=expect):
+        torch.ops.ring_attention_ops.ring_attention_backward(q, q, k, k, k, k, q, l, l, l, sp, 0.125, 0, lens, chunk)
+
+
+def test_autograd_function_rejects_ragged_concatenation():
+    with pytest.raises(ValueError, match="not a multiple of sp_size"):
+        harp_amd.RingAttention.apply(torch.zeros(1, 1, 8, 64), torch.zeros(1, 1, 10, 64), torch.zeros(1, 1, 10, 64), 4)

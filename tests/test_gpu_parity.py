@@ -262,6 +262,33 @@ def test_odd_sizes_and_empty_chunk():
     _check_all(res, ref)
 
 
+@pytest.mark.parametrize("via", ["abi", "ops"])
+def test_very_negative_lse_with_pad_keys(via):
+    """Rows whose every score is far below -88 (LSE about -120), with ragged
+    chunks, so pad keys (zero K / V rows, score 0) sit in the tail tiles.  A
+    pad key's P = exp(0 - LSE) would overflow; the backward must still give
+    finite gradients equal to the oracle's (pad keys excluded by length)."""
+    # Keys spread around u (noise as large as u): with near-identical keys dQ
+    # would be a small residual of cancelling terms that no bf16-operand dS
+    # can resolve to the bar (emulating bf16 dS alone costs 3.5e-2 there, and
+    # 2e-3 here).
+    g = torch.Generator().manual_seed(11)
+    B, H, T, D, N, tc = 1, 2, 40, 64, 2, 100
+    lens = [100, 70]
+    u = torch.randn((1, H, 1, D), generator=g)
+    q = (-20.0 * u + 0.5 * torch.randn((B, H, T, D), generator=g)).to(torch.bfloat16)
+    ks = [(u + torch.randn((B, H, tc, D), generator=g)).to(torch.bfloat16) for _ in range(N)]
+    vs = [torch.randn((B, H, tc, D), generator=g).to(torch.bfloat16) for _ in range(N)]
+    do = torch.randn((B, H, T, D), generator=g).to(torch.bfloat16)
+    scale = 1.0 / math.sqrt(D)
+    ref = _oracle_full(q, ks, vs, do, scale, lens=lens)
+    assert ref["lse"].max() < -100, ref["lse"].max()
+    res = run_hip(q, ks, vs, do, scale, kv_lens=lens, via=via)
+    for name in ("dq", "dk", "dv"):
+        assert torch.isfinite(res[name]).all(), name
+    _check_all(res, ref)
+
+
 def test_nan_propagates_to_its_row_only():
     q, ks, vs, do, scale = _small()
     q = q.clone()
@@ -301,7 +328,7 @@ def test_returns_alias_inputs():
     out = torch.empty(q.shape, device="cuda", dtype=torch.float32)
     m = torch.empty((1, 4, 200, 1), device="cuda", dtype=torch.bfloat16)
     l = torch.empty((1, 4, 200, 1), device="cuda", dtype=torch.float32)
-    r = torch.ops.ring_attention_ops.ring_attention_forward(qd, kd, vd, out, m, l, 3, scale)
+    r = torch.ops.ring_attention_ops.ring_attention_forward(qd, kd, vd, out, m, l, 3, scale, 0, None, 136)
     assert r[0].data_ptr() == out.data_ptr() and r[1].data_ptr() == m.data_ptr() and r[2].data_ptr() == l.data_ptr()
 
 

@@ -1,5 +1,5 @@
-"""GPU test of the sustained-MFMA probe exported by libharp_ra.so (a
-measurement aid with no reference counterpart): it runs, reports a rate
+"""GPU test of the sustained-MFMA probe in the bench-only libharp_probe.so (a
+measurement aid with no reference counterpart, outside the drop-in libraries): it runs, reports a rate
 between a tenth of and the published dense bf16 peak, and a plausible shader
 clock."""
 
