@@ -84,6 +84,8 @@ QK_PROTOTYPES = {
     "harp_qk_norm_rope_forward": (_i, [_p, _i64p, _p, _i, _f, _p, _i64, _i64, _p, _i64p, _p, _i, _i, _i, _i, _p]),
     "harp_qk_norm_rope_backward": (_i, [_p, _i64p, _p, _i64p, _p, _i, _p, _p, _i64, _i64, _p, _i64p, _p, _i,
                                         _i, _i, _i, _i, _p, _sz, _p]),
+    "harp_qk_norm_rope_backward_noalloc": (_i, [_p, _i64p, _p, _i64p, _p, _i, _p, _p, _i64, _i64, _p, _i64p, _p,
+                                                _i, _i, _i, _i, _i, _p]),
     "harp_qk_backward_workspace_bytes": (_sz, [_i, _i, _i, _i]),
     "harp_qk_last_error": (ctypes.c_char_p, []),
 }

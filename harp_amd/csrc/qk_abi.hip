@@ -12,6 +12,7 @@
 #include <cstdio>
 #include <cstring>
 #include <mutex>
+#include <utility>
 #include <string>
 #include <vector>
 
@@ -148,6 +149,38 @@ int resolve_workspace(void** ws, size_t* ws_bytes, size_t need, hipStream_t stre
   return HARP_QK_OK;
 }
 
+// Scratch of the allocation-free backward (harp_qk_norm_rope_backward_noalloc):
+// the weight-gradient partials of at most kQkBwdMaxBlocks row blocks plus their
+// group sums, for any D <= 256: (2048 + 32) x 256 floats = 2.03 MiB, held by
+// every device the library runs on until the process ends.  In host code the
+// name is only a stand-in; kernels get the device address that
+// hipGetSymbolAddress returns for the current device (scratch_ptr below).
+constexpr size_t kScratchFloats =
+    (size_t)(kQkBwdMaxBlocks + (kQkBwdMaxBlocks + kWgGroupRows - 1) / kWgGroupRows) * 256;
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+// Device address of `scratch` on the current device, looked up once per
+// device (with that device current) and kept.
+int scratch_ptr(float** out) {
+  static std::mutex mu;
+  static std::vector<std::pair<int, float*>> table;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(HARP_QK_ELAUNCH, "hipGetDevice failed");
+  std::lock_guard<std::mutex> lk(mu);
+  for (const auto& e : table)
+    if (e.first == dev) {
+      *out = e.second;
+      return HARP_QK_OK;
+    }
+  void* p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !p)
+    return fail(HARP_QK_ELAUNCH, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev, hipGetErrorString(e));
+  table.emplace_back(dev, static_cast<float*>(p));
+  *out = static_cast<float*>(p);
+  return HARP_QK_OK;
+}
+
 int forward(int mode, const void* x, const int64_t* xs, const void* weight, int wdt, float eps, const float* freqs,
             int64_t fsb, int64_t fss, void* out, const int64_t* os, float* rms, int B, int H, int S, int D,
             void* stream) {
@@ -276,6 +309,23 @@ int harp_qk_norm_rope_backward(const void* dy, const int64_t* dy_strides, const 
   return backward(3, dy, dy_strides, x, x_strides, weight, weight_dtype, rms, freqs, f_stride_b, f_stride_s, dx,
                   dx_strides, grad_weight, grad_weight_dtype, batch, h_num, s_len, h_len, workspace,
                   workspace_bytes, stream);
+}
+
+int harp_qk_norm_rope_backward_noalloc(const void* dy, const int64_t* dy_strides, const void* x,
+                                       const int64_t* x_strides, const void* weight, int weight_dtype,
+                                       const float* rms, const float* freqs, int64_t f_stride_b, int64_t f_stride_s,
+                                       void* dx, const int64_t* dx_strides, void* grad_weight, int grad_weight_dtype,
+                                       int batch, int h_num, int s_len, int h_len, void* stream) {
+  int rc;
+  if ((rc = check_shape(batch, h_num, s_len, h_len, true))) return rc;
+  const size_t need = bwd_ws_bytes(QkShape{batch, h_num, s_len, h_len});
+  if (need > sizeof(scratch))
+    return fail(HARP_QK_EUNSUPPORTED, "the weight-gradient partials need %zu bytes, more than the %zu-byte static scratch",
+                need, sizeof(scratch));
+  float* ws = nullptr;
+  if ((rc = scratch_ptr(&ws))) return rc;
+  return backward(3, dy, dy_strides, x, x_strides, weight, weight_dtype, rms, freqs, f_stride_b, f_stride_s, dx,
+                  dx_strides, grad_weight, grad_weight_dtype, batch, h_num, s_len, h_len, ws, sizeof(scratch), stream);
 }
 
 }  // extern "C"

@@ -129,6 +129,24 @@ HARP_QK_API int harp_qk_norm_rope_backward(const void* dy, const int64_t* dy_str
                                            int s_len, int h_len, void* workspace, size_t workspace_bytes,
                                            void* stream);
 
+/*
+ * harp_qk_norm_rope_backward without a workspace argument, and allocating
+ * nothing: no reference counterpart.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  The weight-gradient partials go to a static device
+ * array of the library, 2.03 MiB per device (enough for any h_len <= 256),
+ * held until the process ends; sizes beyond it return HARP_QK_EUNSUPPORTED.
+ * Every call on one device shares that array: calls that overlap on one device
+ * (e.g. on two streams) race and must not be issued; calls ordered on one
+ * stream are safe.  Everything else as harp_qk_norm_rope_backward.
+ */
+HARP_QK_API int harp_qk_norm_rope_backward_noalloc(const void* dy, const int64_t* dy_strides, const void* x,
+                                                   const int64_t* x_strides, const void* weight, int weight_dtype,
+                                                   const float* rms, const float* freqs, int64_t f_stride_b,
+                                                   int64_t f_stride_s, void* dx, const int64_t* dx_strides,
+                                                   void* grad_weight, int grad_weight_dtype, int batch, int h_num,
+                                                   int s_len, int h_len, void* stream);
+
 /* Device workspace the two backward entry points with RMSNorm need
  * ((size_t)-1 when the arguments are invalid): the weight-gradient partial
  * sums of up to 2048 row blocks and their 64-row group sums, at most

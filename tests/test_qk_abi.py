@@ -34,7 +34,7 @@ def header_functions():
 
 def test_header_and_prototypes_agree():
     fns = header_functions()
-    assert len(fns) == 8
+    assert len(fns) == 9
     assert set(fns) == set(_lib.QK_PROTOTYPES)
 
 
