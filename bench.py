@@ -391,7 +391,7 @@ def main() -> int:
     dom = max((n for n in kernel_flops if n in kernels), key=lambda n: kt[n][0])
     dom_tf = kernels[dom]["tflops_algorithmic"]
     fwd_ms = kt["fwd"][0] / args.steps
-    bwd_ms = (kt["dkdv"][0] + kt["dq"][0] + kt["delta"][0]) / args.steps
+    bwd_ms = (kt["stats"][0] + kt["dkdv"][0] + kt["dq"][0] + kt["delta"][0]) / args.steps
 
     result = {
         "metric": "ring-attn fwd+bwd TFLOP/s and % bf16 MFMA peak, S_local=8192 D=128",

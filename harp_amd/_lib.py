@@ -31,7 +31,7 @@ HARP_RA_ELAUNCH = 4
 HARP_RA_F32 = 0
 HARP_RA_BF16 = 1
 HARP_RA_MAX_CHUNKS = 16
-KERNEL_KINDS = ("pack", "fwd", "delta", "dkdv", "dq")
+KERNEL_KINDS = ("stats", "fwd", "delta", "dkdv", "dq")
 
 _lock = threading.Lock()
 _abi: ctypes.CDLL | None = None

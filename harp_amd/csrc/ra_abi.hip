@@ -144,9 +144,14 @@ int make_geometry(int sp_size, int kv_chunk_len, const int32_t* kv_valid_lens, G
   return HARP_RA_OK;
 }
 
-// The kernels stage every operand through LDS and need no device scratch.
+// The forward stages every operand through LDS and needs no device scratch.
+// The backward keeps its per-query statistics, prepared once per call, in
+// two fp32 planes of B*H*T rows (rounded up to 256 bytes).
 size_t fwd_ws(int, int, int, const Geometry&) { return 0; }
-size_t bwd_ws(int, int, int, int, const Geometry&) { return 0; }
+size_t bwd_ws(int batch, int h_num, int t_num, int, const Geometry&) {
+  const size_t bytes = 2 * sizeof(float) * (size_t)batch * h_num * t_num;
+  return (bytes + 255) / 256 * 256;
+}
 
 // Library-owned grow-only workspace, one per device (used when the caller
 // passes workspace == NULL).
@@ -451,6 +456,7 @@ int harp_ra_backward(const void* q, const int64_t* q_strides, void* grad_q, cons
   p.T = t_num;
   p.D = h_len;
   p.scale = scale;
+  p.inv_scale = 1.f / scale;
   p.ct.n = sp_size;
   int key_tiles = 0;
   for (int c = 0; c < sp_size; ++c) {
@@ -467,6 +473,11 @@ int harp_ra_backward(const void* q, const int64_t* q_strides, void* grad_q, cons
   p.n_key_tiles = key_tiles;
   if ((int64_t)key_tiles * h_num * batch > INT32_MAX || (int64_t)((t_num + 127) / 128) * h_num * batch > INT32_MAX)
     return fail(HARP_RA_EUNSUPPORTED, "grid too large");
+  p.stats = static_cast<float*>(workspace);
+  {
+    TimedLaunch tl(HARP_RA_KERNEL_STATS, st);
+    if ((rc = launched(launch_stats_prep(p, st), "statistics preparation"))) return rc;
+  }
   {
     TimedLaunch tl(HARP_RA_KERNEL_DKDV, st);
     if ((rc = launched(launch_dkdv(p, st), "dK/dV"))) return rc;

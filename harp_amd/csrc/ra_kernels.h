@@ -46,10 +46,12 @@ struct BwdParams {
   int m_bf16;
   const float* l;
   const float* delta;
+  float* stats;             // workspace [2][B*H*T]: -(m + ln l) / scale, -D (stats_prep_kernel)
   int n_key_tiles;          // kDkdvBlockKeys-key blocks per (b, h) over all chunks
   int ct_rows[kMaxChunks];  // stored rows of chunk c (dK/dV rows written, pads get 0)
   int B, H, T, D;
   float scale;
+  float inv_scale;  // 1 / scale (a kernel argument, so it stays in an SGPR)
   ChunkTable ct;
 };
 
@@ -58,6 +60,7 @@ constexpr int kDkdvBlockKeys = 256;
 
 hipError_t launch_fwd(const FwdParams& p, hipStream_t st);
 hipError_t launch_delta(const DeltaParams& p, hipStream_t st);
+hipError_t launch_stats_prep(const BwdParams& p, hipStream_t st);
 hipError_t launch_dq(const BwdParams& p, hipStream_t st);
 hipError_t launch_dkdv(const BwdParams& p, hipStream_t st);
 

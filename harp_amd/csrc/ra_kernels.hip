@@ -113,6 +113,17 @@ __device__ __forceinline__ void lds_dma_b128(rsrc_t rs, uint32_t lds, uint32_t v
       : "memory", "m0");
 }
 
+// The same with 4 bytes per lane: lane i's dword lands at lds + 4 * i.
+__device__ __forceinline__ void lds_dma_b32(rsrc_t rs, uint32_t lds, uint32_t voff) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dword %1, %2, 0 offen lds"
+      :
+      : "s"(lds), "v"(voff), "s"(rs)
+      : "memory", "m0");
+}
+
 // Wait for this thread's direct-to-LDS loads (a barrier then publishes them).
 __device__ __forceinline__ void wait_lds_loads() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
@@ -628,12 +639,20 @@ __global__ __launch_bounds__(256) void delta_kernel(DeltaParams p) {
   if (row < rows && sub == 0) p.delta[row] = acc;
 }
 
-// Per-query log2-domain LSE from the forward's (m, l): (m + ln l) * log2(e).
-// Rows with l <= 0 (no valid key) get +inf so that P = exp2(s - inf) = 0.
-__device__ __forceinline__ float lse2_of(const void* m, int m_bf16, const float* l, int64_t i) {
-  const float mm = m_bf16 ? (float)((const bf16*)m)[i] : ((const float*)m)[i];
-  const float ll = l[i];
-  return (ll > 0.f) ? (mm + __logf(ll)) * kLog2e : INFINITY;
+// ---------------------------------------------------------------------------
+// Backward statistics, once per call, in the form both backward kernels read:
+// plane 0 = -(m + ln l) / scale per query (-inf for a row with l <= 0, which
+// then gets P = 0), plane 1 = -D.  With S' = Q K^T + plane 0 and
+// dP' = dO V^T + plane 1, P = exp2(S' c) and dS = P dP'.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void stats_prep_kernel(BwdParams p) {
+  const int64_t n = (int64_t)p.B * p.H * p.T;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const float mm = p.m_bf16 ? (float)((const bf16*)p.m)[i] : ((const float*)p.m)[i];
+  const float ll = p.l[i];
+  p.stats[i] = (ll > 0.f) ? -(mm + __logf(ll)) * p.inv_scale : -INFINITY;
+  p.stats[n + i] = -p.delta[i];
 }
 
 // ---------------------------------------------------------------------------
@@ -687,8 +706,10 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
     }
   }
   const int64_t si = ((int64_t)b * p.H + h) * p.T + qi;
-  const float lse2 = q_ok ? lse2_of(p.m, p.m_bf16, p.l, si) : INFINITY;
-  const float dlt = q_ok ? p.delta[si] : 0.f;
+  const int64_t nrows = (int64_t)p.B * p.H * p.T;
+  // LSE2 = -c * plane 0 (+inf for a row without keys); D = -plane 1
+  const float lse2 = q_ok ? -p.stats[si] * c2 : INFINITY;
+  const float dlt = q_ok ? -p.stats[nrows + si] : 0.f;
   XorLanes<DP, KSTEPS> klo;
   klo.init_rows_lean(lane);
   klo.init_tr_lean(lane);
@@ -849,11 +870,13 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
 // ---------------------------------------------------------------------------
 // Block = 8 waves x 32 keys (256 keys; two waves per SIMD, one block per CU).
 // Each wave keeps its 32 K rows as MFMA B operands in registers and reads
-// its V rows from the block's LDS copy; dK, dV accumulate in fp32 AGPRs over
-// every query.  Queries stream in 64-row tiles (Q, dO, per-row LSE2 and D)
+// its V rows from the block's LDS copy; dK, dV accumulate in fp32 VGPRs over
+// every query.  Queries stream in 64-row tiles (Q, dO, per-row statistics)
 // through double-buffered LDS; per 32-query half:
-//   A: S = Q K^T, dP = dO V^T      (C row = query, col = key)
-//   B: P = exp2(S c - LSE2), dS = P (dP - D)
+//   A: S' = Q K^T - LSE2 / c, dP' = dO V^T - D   (C row = query, col = key;
+//      the per-row terms are the accumulators' initial values, read from
+//      LDS, so the softmax needs no per-row broadcast)
+//   B: P = exp2(S' c), dS = P dP'
 //   C: dV += P^T dO, dK += dS^T Q  (P / dS straight from the accumulator
 //      layout as A operands; dO^T, Q^T by transposed LDS reads)
 // Two waves per SIMD hide each other's VALU and LDS latency, and one LDS
@@ -874,7 +897,9 @@ __global__ __launch_bounds__(64 * kDkWaves, 1) void dkdv_kernel(BwdParams p) {
   // two Q / dO buffers; before the loop they hold the block's K rows (as
   // NVT XorTiles) while each wave copies its K fragments into registers
   __shared__ __attribute__((aligned(16))) bf16 QG[2][2][GQ::ELEMS];  // [buffer][Q, dO]
-  __shared__ __attribute__((aligned(16))) float St[2][128];            // per query: (LSE2, D)
+  // per query of a tile: the initial values of the S' and dP' accumulators
+  // (the prepared planes: -LSE2 / c and -D), [buffer][S', dP'][query]
+  __shared__ __attribute__((aligned(16))) float St[2][2][64];
   static_assert(NVT <= 4, "K staging uses the four Q / dO tile slots");
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -889,6 +914,7 @@ __global__ __launch_bounds__(64 * kDkWaves, 1) void dkdv_kernel(BwdParams p) {
   const int key0 = kblk0 + wave * 32;
   const int len = p.ct.len[c];
   const float c2 = p.scale * kLog2e;
+
 
   f32x16 dk[DBLK], dv[DBLK];
 #pragma unroll
@@ -909,27 +935,25 @@ __global__ __launch_bounds__(64 * kDkWaves, 1) void dkdv_kernel(BwdParams p) {
     const bf16* qb_ = p.q + (int64_t)b * p.sqb + (int64_t)h * p.sqh;
     const bf16* gb_ = p.dout + (int64_t)b * p.sdb + (int64_t)h * p.sdh;
     const int64_t sbase = ((int64_t)b * p.H + h) * p.T;
+    const int64_t nrows = (int64_t)p.B * p.H * p.T;
 
-    // Per-query statistics of the next tile: wave 0 loads the raw m / l / D
-    // bits when it issues the tile and converts them only in store_stats,
-    // after the wait that precedes the barrier.
-    uint32_t m_bits = 0, l_bits = 0, d_bits = 0;
-    auto issue_stats = [&](int q0) {
-      if (tid < 64) {
-        const int qq = q0 + tid;
-        m_bits = l_bits = d_bits = 0;  // l = 0 marks a row past T: P = 0
-        if (qq < p.T) {
-          const int64_t i = sbase + qq;
-          m_bits = p.m_bf16 ? (uint32_t)((const uint16_t*)p.m)[i] : ((const uint32_t*)p.m)[i];
-          l_bits = ((const uint32_t*)p.l)[i];
-          d_bits = ((const uint32_t*)p.delta)[i];
+    // Per-query statistics of a tile (the two prepared planes, 64 rows each)
+    // go global -> LDS by two dword copies of wave 0.  Rows past T read as 0:
+    // their Q and dO rows are zero too, so P dO and dS = P dP' vanish.
+    auto issue_stats = [&](int q0, int bf) {
+      if (wave == 0) {
+        const uint32_t voff = (uint32_t)lane * 4u;
+#pragma unroll
+        for (int pl = 0; pl < 2; ++pl) {
+          const rsrc_t rs = make_rsrc(p.stats + pl * nrows + sbase + q0, (uint32_t)(p.T - q0) * 4u);
+          lds_dma_b32(rs, (uint32_t)(uintptr_t)(lds_void*)&St[bf][pl][0], voff);
         }
       }
     };
     auto issue = [&](int q0, int bf) {
       qld.load(rows_rsrc(qb_, p.sqt, q0, p.T - q0), QG[bf][0]);
       gld.load(rows_rsrc(gb_, p.sdt, q0, p.T - q0), QG[bf][1]);
-      issue_stats(q0);
+      issue_stats(q0, bf);
     };
     // Inside the loop the next tile's copies are issued one instruction per
     // MFMA step of the first S / dP phase rather than in one burst after
@@ -939,14 +963,6 @@ __global__ __launch_bounds__(64 * kDkWaves, 1) void dkdv_kernel(BwdParams p) {
     constexpr int kSlotsQ = DirectLoader<GQ, kDkWaves>::kInst, kDmaSlots = 2 * kSlotsQ;
     constexpr int kSlotsPerStep = (kDmaSlots + KSTEPS - 1) / KSTEPS;
     rsrc_t nq_rs, ng_rs;
-    auto store_stats = [&](int bf) {
-      if (tid < 64) {
-        const float mm = __uint_as_float(p.m_bf16 ? m_bits << 16 : m_bits);
-        const float ll = __uint_as_float(l_bits);
-        const float lse2 = (ll > 0.f) ? (mm + __logf(ll)) * kLog2e : INFINITY;
-        *(float2*)&St[bf][2 * tid] = make_float2(lse2, __uint_as_float(d_bits));
-      }
-    };
 
     bf16x8 kf[KSTEPS];
     {
@@ -972,13 +988,19 @@ __global__ __launch_bounds__(64 * kDkWaves, 1) void dkdv_kernel(BwdParams p) {
     const bf16* Vw = Vb[wave >> 1];
     const int vrb = wave & 1;
     issue(0, 0);
-    store_stats(0);  // (waits for wave 0's statistics loads)
 
-    // (LSE2, D) of query row c_row(lane % 16, g) of half qb: one read per lane
-    // per half; row_bcast then hands each C register r the values of its own
-    // row c_row(r, g).
-    auto stats_lane = [&](int bf, int qb) {
-      return *(const float2*)&St[bf][2 * (qb * 32 + c_row(lane & 15, g))];
+    // Initial accumulator of half qb from LDS row values: register 4j + i of
+    // lane-half g holds row c_row(4j + i, g) = 8j + 4g + i, so four 16-byte
+    // reads (the same address for all 32 lanes of a half) fill the tile.
+    auto init_rows = [&](const float* col, int qb) {
+      f32x16 x;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const f32x4 v = *(const f32x4*)(col + qb * 32 + 8 * j + 4 * g);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[4 * j + i] = v[i];
+      }
+      return x;
     };
     const int n_tiles = (p.T + 63) >> 6;
     int buf = 0;
@@ -996,14 +1018,15 @@ __global__ __launch_bounds__(64 * kDkWaves, 1) void dkdv_kernel(BwdParams p) {
       const bf16* Gd = QG[buf][1];
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb) {
-        const float2 st = stats_lane(buf, qb);
         if (qb == 0) prio<3>();
         else prio<1>();
-        f32x16 s = zero16(), dp = zero16();
+        f32x16 s = init_rows(St[buf][0], qb), dp = init_rows(St[buf][1], qb);
         pipelined<KSTEPS, 1>(
-            [&](int ks) { return Frag2{lo.row_frag_lean(Q, qb, ks), lo.row_frag_lean(Gd, qb, ks)}; },
-            [&](int ks, const Frag2& f) {
-              const bf16x8 v = vlo.frag(Vw, vrb, ks);
+            [&](int ks) {
+              return Frag3{lo.row_frag_lean(Q, qb, ks), lo.row_frag_lean(Gd, qb, ks), vlo.frag(Vw, vrb, ks)};
+            },
+            [&](int ks, const Frag3& f) {
+              const bf16x8 v = f.c;
               s = mfma32x32x16(f.a, kf[ks], s);
               if (qb == 0 && has_next) {
 #pragma unroll
@@ -1012,7 +1035,7 @@ __global__ __launch_bounds__(64 * kDkWaves, 1) void dkdv_kernel(BwdParams p) {
                   if (j < kSlotsQ) qld.load_one(nq_rs, QG[buf ^ 1][0], j);
                   else if (j < kDmaSlots) gld.load_one(ng_rs, QG[buf ^ 1][1], j - kSlotsQ);
                 }
-                if (ks == KSTEPS - 1) issue_stats(nq0);
+                if (ks == KSTEPS - 1) issue_stats(nq0, buf ^ 1);
               }
               dp = mfma32x32x16(f.b, v, dp);
             });
@@ -1021,9 +1044,9 @@ __global__ __launch_bounds__(64 * kDkWaves, 1) void dkdv_kernel(BwdParams p) {
         bf16x8 pf[2], dsf[2];
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const float pv = exp2_unit(__builtin_fmaf(s[r], c2, -row_bcast(st.x, r)));
+          const float pv = exp2_unit(s[r] * c2);
           pf[r >> 3][r & 7] = (bf16)pv;
-          dsf[r >> 3][r & 7] = (bf16)(pv * (dp[r] - row_bcast(st.y, r)));
+          dsf[r >> 3][r & 7] = (bf16)(pv * dp[r]);
         }
         if (qb == 0) prio<2>();
         else prio<0>();
@@ -1041,7 +1064,6 @@ __global__ __launch_bounds__(64 * kDkWaves, 1) void dkdv_kernel(BwdParams p) {
             });
       }
       prio<0>();
-      if (t + 1 < n_tiles) store_stats(buf ^ 1);
       buf ^= 1;
     }
   }
@@ -1070,6 +1092,12 @@ __global__ __launch_bounds__(64 * kDkWaves, 1) void dkdv_kernel(BwdParams p) {
       }
     }
   }
+}
+
+hipError_t launch_stats_prep(const BwdParams& p, hipStream_t st) {
+  const int64_t n = (int64_t)p.B * p.H * p.T;
+  hipLaunchKernelGGL(stats_prep_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, p);
+  return hipGetLastError();
 }
 
 // Every (KSTEPS, DBLK) variant the launchers dispatch to, instantiated

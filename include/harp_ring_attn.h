@@ -83,6 +83,10 @@ HARP_RA_API int harp_ra_forward(const void* q, const int64_t* q_strides,
  *   int h_num, int h_len, int sp_size, float* m_i, float* l_i, float* D,
  *   float scale) — gemm/ring_attention/ring_attn.cpp:2577-2581, called from
  *   ring_attention_backward_op, torch_ring_attention_ops.cpp:217-257.
+ * workspace: harp_ra_backward_workspace_bytes() bytes of device memory
+ * (256-byte aligned), or NULL to use a grow-only per-device buffer owned by
+ * the library (calls with a NULL workspace that overlap on one device then
+ * race; that path may call hipMalloc, so graph-captured calls pass one).
  */
 HARP_RA_API int harp_ra_backward(const void* q, const int64_t* q_strides,
                      void* grad_q, const int64_t* dq_strides, int dq_dtype,
@@ -110,8 +114,10 @@ HARP_RA_API int harp_ra_delta(const void* grad_out, const int64_t* do_strides,
 
 /*
  * Device workspace the forward / backward need for these sizes ((size_t)-1
- * when the arguments are invalid; 0 = none needed, the current kernels keep
- * all staging in LDS).  Replaces the reference's grow-only scratch sizing
+ * when the arguments are invalid; 0 = none needed).  The forward keeps all
+ * staging in LDS and needs none; the backward needs 8 bytes per query row
+ * (B*H*T, rounded up to 256 bytes) for its per-query statistics, prepared
+ * once per call.  Replaces the reference's grow-only scratch sizing
  * (RingAttnHbmWorkspace::ensure_slot, ring_attn.cpp:620-840, sized at
  * :2428-2450 and :2595-2656).
  */
@@ -135,7 +141,7 @@ HARP_RA_API const char* harp_ra_last_error(void);
  * last read, then clears them.  Not thread-safe with concurrent calls.
  */
 enum {
-  HARP_RA_KERNEL_PACK = 0, /* reserved: operand repacking (unused by the current kernels) */
+  HARP_RA_KERNEL_STATS = 0, /* the backward's per-query statistics preparation */
   HARP_RA_KERNEL_FWD = 1,
   HARP_RA_KERNEL_DELTA = 2,
   HARP_RA_KERNEL_DKDV = 3,
