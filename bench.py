@@ -255,6 +255,42 @@ def producer_bench(cfg, seed: int, iters: int = 20):
         "tflops_incl_norm_rope": round(gemm_flop / (ms * 1e-3) / 1e12, 1),
         "what": f"3 projections [{B},{T},{dim}] x [{dim},{dim}] (torch Linear, hipBLASLt) + fused norm+RoPE of q and k",
     }
+
+    # the parts on their own, and the alternative of one GEMM over the
+    # concatenated q/k/v weights (N = 3 * dim) followed by the same passes
+    def timed(fn, n=iters):
+        for _ in range(3):
+            fn()
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        torch.cuda.synchronize()
+        e[0].record()
+        for _ in range(n):
+            fn()
+        e[1].record()
+        torch.cuda.synchronize()
+        return e[0].elapsed_time(e[1]) / n
+
+    w_cat = torch.cat([m.weight for m in lin], 0)
+    qkv = torch.empty((B, T, 3 * dim), device=dev, dtype=torch.bfloat16)
+    q_out = torch.empty((B, T, dim), device=dev, dtype=torch.bfloat16).unflatten(-1, (H, D)).transpose(1, 2)
+    k_out = torch.empty_like(q_out)
+    rms_q = torch.empty(B * H * T, device=dev, dtype=torch.float32)
+    with torch.no_grad():
+        ms_3 = timed(lambda: [m(hid) for m in lin])
+        ms_cat = timed(lambda: torch.matmul(hid, w_cat.t(), out=qkv))
+        qv = qkv[..., :dim].unflatten(-1, (H, D)).transpose(1, 2)
+        kv = qkv[..., dim:2 * dim].unflatten(-1, (H, D)).transpose(1, 2)
+        ms_nr = timed(lambda: (ops.qk_norm_rope_forward(qv, w, freqs, q_out, rms_q, 1e-6),
+                               ops.qk_norm_rope_forward(kv, w, freqs, k_out, rms_q, 1e-6)))
+    res["producer_parts"] = {
+        "three_gemms_ms": round(ms_3, 4),
+        "three_gemms_tflops": round(gemm_flop / (ms_3 * 1e-3) / 1e12, 1),
+        "one_concatenated_gemm_ms": round(ms_cat, 4),
+        "one_concatenated_gemm_tflops": round(gemm_flop / (ms_cat * 1e-3) / 1e12, 1),
+        "norm_rope_q_and_k_ms": round(ms_nr, 4),
+        "norm_rope_q_and_k_bytes": int(2 * fwd_bytes),
+        "norm_rope_q_and_k_frac_hbm_peak": round(2 * fwd_bytes / (ms_nr * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+    }
     return res
 
 

@@ -25,5 +25,6 @@ from .ops import (  # noqa: F401
 from .qk import ApplyRotaryComplexFn, QKNormRopeFn, RMSNormFn  # noqa: F401
 from .attention import RingZAttention, project_qkv  # noqa: F401
 from .wait_engine import CommWork, WaitEngine  # noqa: F401
+from .gemm import xhblas_gemm  # noqa: F401
 
 __version__ = "0.1.0"
