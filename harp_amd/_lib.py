@@ -60,7 +60,7 @@ ABI_PROTOTYPES = {
          _i, _i, _i, _i, _i, _i, ctypes.c_float, _p, _sz, _p],
     ),
     "harp_ra_delta": (_i, [_p, _i64p, _p, _i64p, _p, _i, _i, _i, _i, _p]),
-    "harp_ra_forward_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i32p]),
+    "harp_ra_forward_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i, _i32p]),
     "harp_ra_backward_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i, _i32p]),
     "harp_ra_timing_enable": (_i, [_i]),
     "harp_ra_timing_read": (_i, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int), _i]),

@@ -144,13 +144,63 @@ int make_geometry(int sp_size, int kv_chunk_len, const int32_t* kv_valid_lens, G
   return HARP_RA_OK;
 }
 
-// The forward stages every operand through LDS and needs no device scratch.
-// The backward keeps its per-query statistics, prepared once per call, in
-// two fp32 planes of B*H*T rows (rounded up to 256 bytes).
-size_t fwd_ws(int, int, int, const Geometry&) { return 0; }
-size_t bwd_ws(int batch, int h_num, int t_num, int, const Geometry&) {
-  const size_t bytes = 2 * sizeof(float) * (size_t)batch * h_num * t_num;
-  return (bytes + 255) / 256 * 256;
+size_t round256(size_t bytes) { return (bytes + 255) / 256 * 256; }
+
+// Compute units of the current device (0 if the query fails).
+int device_cus() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  return cus;
+}
+
+// KV splits of the forward and dQ kernels.  Their grids have one 8-wave
+// block (one CU) per 256-query tile and (b, h); when that leaves at least
+// half of the CUs idle, each tile's ring steps are split over up to N blocks
+// (never more splits than chunks), whose partial results are merged after.
+int kv_splits(int batch, int h_num, int t_num, const Geometry& g) {
+  const int64_t blocks = (int64_t)((t_num + kQueryBlockRows - 1) / kQueryBlockRows) * h_num * batch;
+  const int cus = device_cus();
+  if (g.n < 2 || cus < 2 || blocks * 2 > cus) return 1;
+  const int64_t fill = cus / blocks;
+  return (int)(fill < g.n ? fill : g.n);
+}
+
+// Forward: no scratch, except the KV splits' partial O (fp32 [n][B,H,T,D])
+// and row statistics (fp32 m and l, [n][B,H,T] each).
+struct FwdLayout {
+  int n_split;
+  size_t o, m, l, bytes;  // byte offsets
+};
+FwdLayout fwd_layout(int batch, int h_num, int t_num, int h_len, const Geometry& g) {
+  FwdLayout w{kv_splits(batch, h_num, t_num, g), 0, 0, 0, 0};
+  if (w.n_split < 2) return w;
+  const size_t rows = (size_t)batch * h_num * t_num;
+  w.m = round256(sizeof(float) * w.n_split * rows * h_len);
+  w.l = w.m + round256(sizeof(float) * w.n_split * rows);
+  w.bytes = w.l + round256(sizeof(float) * w.n_split * rows);
+  return w;
+}
+size_t fwd_ws(int batch, int h_num, int t_num, int h_len, const Geometry& g) {
+  return fwd_layout(batch, h_num, t_num, h_len, g).bytes;
+}
+
+// Backward: the per-query statistics, prepared once per call, in two fp32
+// planes of B*H*T rows; then, with KV splits, the dQ kernel's partials
+// (fp32 [n][B,H,T,D]).
+struct BwdLayout {
+  int n_split;
+  size_t stats, dq, bytes;  // byte offsets
+};
+BwdLayout bwd_layout(int batch, int h_num, int t_num, int h_len, const Geometry& g) {
+  BwdLayout w{kv_splits(batch, h_num, t_num, g), 0, 0, 0};
+  const size_t rows = (size_t)batch * h_num * t_num;
+  w.dq = round256(2 * sizeof(float) * rows);
+  w.bytes = w.dq + (w.n_split > 1 ? round256(sizeof(float) * w.n_split * rows * h_len) : 0);
+  return w;
+}
+size_t bwd_ws(int batch, int h_num, int t_num, int h_len, const Geometry& g) {
+  return bwd_layout(batch, h_num, t_num, h_len, g).bytes;
 }
 
 // Library-owned grow-only workspace, one per device (used when the caller
@@ -282,12 +332,12 @@ int harp_ra_timing_read(double* ms, int* launches, int n_kinds) {
   return ok();
 }
 
-size_t harp_ra_forward_workspace_bytes(int batch, int h_num, int h_len, int sp_size, int kv_chunk_len,
+size_t harp_ra_forward_workspace_bytes(int batch, int h_num, int t_num, int h_len, int sp_size, int kv_chunk_len,
                                        const int32_t* kv_valid_lens) {
   Geometry g;
-  if (check_dims(batch, h_num, 1, h_len) != HARP_RA_OK) return SIZE_MAX;
+  if (check_dims(batch, h_num, t_num, h_len) != HARP_RA_OK) return SIZE_MAX;
   if (make_geometry(sp_size, kv_chunk_len, kv_valid_lens, &g) != HARP_RA_OK) return SIZE_MAX;
-  return fwd_ws(batch, h_num, h_len, g);
+  return fwd_ws(batch, h_num, t_num, h_len, g);
 }
 
 size_t harp_ra_backward_workspace_bytes(int batch, int h_num, int t_num, int h_len, int sp_size, int kv_chunk_len,
@@ -321,8 +371,8 @@ int harp_ra_forward(const void* q, const int64_t* q_strides, const void* const* 
   if (!m_i || !l_i) return fail(HARP_RA_EINVAL, "m_i / l_i are NULL");
   if (m_i_dtype != HARP_RA_F32 && m_i_dtype != HARP_RA_BF16) return fail(HARP_RA_EINVAL, "m_i_dtype must be F32 or BF16");
 
-  const size_t need = fwd_ws(batch, h_num, h_len, g);
-  if ((rc = resolve_workspace(&workspace, &workspace_bytes, need))) return rc;
+  const FwdLayout wl = fwd_layout(batch, h_num, t_num, h_len, g);
+  if ((rc = resolve_workspace(&workspace, &workspace_bytes, wl.bytes))) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
 
   FwdParams p;
@@ -353,9 +403,42 @@ int harp_ra_forward(const void* q, const int64_t* q_strides, const void* const* 
     p.ct.len[c] = g.len[c];
     p.ct.order[c] = (c + ring_rank) % sp_size;
   }
+  p.n_split = wl.n_split;
+  FwdMergeParams mp;
+  std::memset(&mp, 0, sizeof(mp));
+  if (wl.n_split > 1) {
+    // the kernel writes per-split partials (fp32, [n][B,H,T,D] and [n][B,H,T]);
+    // the merge writes out / m_i / l_i
+    char* ws = static_cast<char*>(workspace);
+    mp.part_o = reinterpret_cast<const float*>(ws + wl.o);
+    mp.part_m = reinterpret_cast<const float*>(ws + wl.m);
+    mp.part_l = reinterpret_cast<const float*>(ws + wl.l);
+    mp.n_split = wl.n_split;
+    mp.out = out;
+    mp.sob = p.sob;
+    mp.soh = p.soh;
+    mp.sot = p.sot;
+    mp.m = m_i;
+    mp.m_bf16 = p.m_bf16;
+    mp.l = l_i;
+    mp.B = batch;
+    mp.H = h_num;
+    mp.T = t_num;
+    mp.D = h_len;
+    p.out = reinterpret_cast<float*>(ws + wl.o);
+    p.sot = h_len;
+    p.soh = (int64_t)t_num * h_len;
+    p.sob = (int64_t)h_num * p.soh;
+    p.split_o = (int64_t)batch * p.sob;
+    p.m = ws + wl.m;
+    p.m_bf16 = 0;
+    p.l = reinterpret_cast<float*>(ws + wl.l);
+    p.split_ml = (int64_t)batch * h_num * t_num;
+  }
   {
-    TimedLaunch tl(HARP_RA_KERNEL_FWD, st);
+    TimedLaunch tl(HARP_RA_KERNEL_FWD, st);  // the merge is timed with the forward
     if ((rc = launched(launch_fwd(p, st), "forward"))) return rc;
+    if (wl.n_split > 1 && (rc = launched(launch_fwd_merge(mp, st), "forward merge"))) return rc;
   }
   return ok();
 }
@@ -421,8 +504,8 @@ int harp_ra_backward(const void* q, const int64_t* q_strides, void* grad_q, cons
   if (!m_i || !l_i || !delta) return fail(HARP_RA_EINVAL, "m_i / l_i / delta are NULL");
   if (m_i_dtype != HARP_RA_F32 && m_i_dtype != HARP_RA_BF16) return fail(HARP_RA_EINVAL, "m_i_dtype must be F32 or BF16");
 
-  const size_t need = bwd_ws(batch, h_num, t_num, h_len, g);
-  if ((rc = resolve_workspace(&workspace, &workspace_bytes, need))) return rc;
+  const BwdLayout wl = bwd_layout(batch, h_num, t_num, h_len, g);
+  if ((rc = resolve_workspace(&workspace, &workspace_bytes, wl.bytes))) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
 
   BwdParams p;
@@ -473,7 +556,9 @@ int harp_ra_backward(const void* q, const int64_t* q_strides, void* grad_q, cons
   p.n_key_tiles = key_tiles;
   if ((int64_t)key_tiles * h_num * batch > INT32_MAX || (int64_t)((t_num + 127) / 128) * h_num * batch > INT32_MAX)
     return fail(HARP_RA_EUNSUPPORTED, "grid too large");
-  p.stats = static_cast<float*>(workspace);
+  char* ws = static_cast<char*>(workspace);
+  p.stats = reinterpret_cast<float*>(ws + wl.stats);
+  p.n_split = 1;
   {
     TimedLaunch tl(HARP_RA_KERNEL_STATS, st);
     if ((rc = launched(launch_stats_prep(p, st), "statistics preparation"))) return rc;
@@ -482,9 +567,33 @@ int harp_ra_backward(const void* q, const int64_t* q_strides, void* grad_q, cons
     TimedLaunch tl(HARP_RA_KERNEL_DKDV, st);
     if ((rc = launched(launch_dkdv(p, st), "dK/dV"))) return rc;
   }
+  DqMergeParams mp;
+  std::memset(&mp, 0, sizeof(mp));
+  if (wl.n_split > 1) {
+    // per-split fp32 partials [n][B,H,T,D], summed into grad_q by the merge
+    mp.part = reinterpret_cast<const float*>(ws + wl.dq);
+    mp.n_split = wl.n_split;
+    mp.dq = grad_q;
+    mp.sdqb = p.sdqb;
+    mp.sdqh = p.sdqh;
+    mp.sdqt = p.sdqt;
+    mp.dq_f32 = p.dq_f32;
+    mp.B = batch;
+    mp.H = h_num;
+    mp.T = t_num;
+    mp.D = h_len;
+    p.n_split = wl.n_split;
+    p.dq = ws + wl.dq;
+    p.dq_f32 = 1;
+    p.sdqt = h_len;
+    p.sdqh = (int64_t)t_num * h_len;
+    p.sdqb = (int64_t)h_num * p.sdqh;
+    p.split_dq = (int64_t)batch * p.sdqb;
+  }
   {
-    TimedLaunch tl(HARP_RA_KERNEL_DQ, st);
+    TimedLaunch tl(HARP_RA_KERNEL_DQ, st);  // the merge is timed with the dQ kernel
     if ((rc = launched(launch_dq(p, st), "dQ"))) return rc;
+    if (wl.n_split > 1 && (rc = launched(launch_dq_merge(mp, st), "dQ merge"))) return rc;
   }
   return ok();
 }

@@ -19,7 +19,36 @@ struct FwdParams {
   float* l;               // [B,H,T] contiguous
   int B, H, T, D;
   float scale;
+  int n_split;            // KV splits (grid dimension y); > 1: out / m / l are per-split partials
+  int64_t split_o;        // elements between the splits' out buffers
+  int64_t split_ml;       // elements between the splits' m / l buffers
   ChunkTable ct;
+};
+
+// Combines the KV splits of the forward: per query row, the splits'
+// normalised O, row max m and sum l (fp32, [n][B,H,T(,D)] contiguous) merge
+// as O = sum_s w_s O_s / sum_s w_s with w_s = l_s exp(m_s - max_s m_s).
+struct FwdMergeParams {
+  const float* part_o;
+  const float* part_m;
+  const float* part_l;
+  int n_split;
+  float* out;
+  int64_t sob, soh, sot;
+  void* m;
+  int m_bf16;
+  float* l;
+  int B, H, T, D;
+};
+
+// Sums the KV splits' dQ partials (fp32, already scaled, [n][B,H,T,D]).
+struct DqMergeParams {
+  const float* part;
+  int n_split;
+  void* dq;
+  int64_t sdqb, sdqh, sdqt;
+  int dq_f32;
+  int B, H, T, D;
 };
 
 struct DeltaParams {
@@ -47,6 +76,8 @@ struct BwdParams {
   const float* l;
   const float* delta;
   float* stats;             // workspace [2][B*H*T]: -(m + ln l) / scale, -D (stats_prep_kernel)
+  int n_split;              // KV splits of the dQ kernel (grid dimension y); > 1: dq is per-split partials
+  int64_t split_dq;         // elements between the splits' dQ buffers
   int n_key_tiles;          // kDkdvBlockKeys-key blocks per (b, h) over all chunks
   int ct_rows[kMaxChunks];  // stored rows of chunk c (dK/dV rows written, pads get 0)
   int B, H, T, D;
@@ -59,6 +90,10 @@ struct BwdParams {
 constexpr int kDkdvBlockKeys = 256;
 
 hipError_t launch_fwd(const FwdParams& p, hipStream_t st);
+hipError_t launch_fwd_merge(const FwdMergeParams& p, hipStream_t st);
+hipError_t launch_dq_merge(const DqMergeParams& p, hipStream_t st);
+// Query rows per block of the forward and dQ kernels (the host sizes KV splits with it).
+constexpr int kQueryBlockRows = 256;
 hipError_t launch_delta(const DeltaParams& p, hipStream_t st);
 hipError_t launch_stats_prep(const BwdParams& p, hipStream_t st);
 hipError_t launch_dq(const BwdParams& p, hipStream_t st);

@@ -386,12 +386,13 @@ struct KvCursor {
   const bf16* k;
   const bf16* v;
 };
-// first non-empty chunk from ring step `step` on (step == ct.n: past the end)
-__device__ __forceinline__ void kv_enter(const ChunkTable& ct, int64_t kvo, int step, KvCursor& c) {
-  while (step < ct.n && ct.len[ct.order[step]] == 0) ++step;
+// first non-empty chunk from ring step `step` on, before step `end`
+// (step == end: past the end)
+__device__ __forceinline__ void kv_enter(const ChunkTable& ct, int64_t kvo, int step, int end, KvCursor& c) {
+  while (step < end && ct.len[ct.order[step]] == 0) ++step;
   c.step = step;
   c.k0 = 0;
-  if (step < ct.n) {
+  if (step < end) {
     const int ch = ct.order[step];
     c.len = ct.len[ch];
     c.k = ct.k[ch] + kvo;
@@ -399,11 +400,24 @@ __device__ __forceinline__ void kv_enter(const ChunkTable& ct, int64_t kvo, int 
   }
 }
 // the tile after the one of tile_keys keys at c
-__device__ __forceinline__ KvCursor kv_next(const ChunkTable& ct, int64_t kvo, const KvCursor& c, int tile_keys) {
+__device__ __forceinline__ KvCursor kv_next(const ChunkTable& ct, int64_t kvo, const KvCursor& c, int tile_keys,
+                                             int end) {
   KvCursor n = c;
   n.k0 = c.k0 + tile_keys;
-  if (n.k0 >= c.len) kv_enter(ct, kvo, c.step + 1, n);
+  if (n.k0 >= c.len) kv_enter(ct, kvo, c.step + 1, end, n);
   return n;
+}
+
+// KV split (grid dimension y): split s of n visits ring steps
+// [s * N / n, (s + 1) * N / n) and writes its results at offset s times the
+// split stride of its output buffers (the host points those at per-split
+// partial buffers; with n == 1 this is the whole ring and offset 0).
+struct KvSplit {
+  int begin, end, index;
+};
+__device__ __forceinline__ KvSplit kv_split(int n_chunks) {
+  const int s = (int)blockIdx.y, n = (int)gridDim.y;
+  return KvSplit{s * n_chunks / n, (s + 1) * n_chunks / n, s};
 }
 
 // ---------------------------------------------------------------------------
@@ -414,6 +428,7 @@ __device__ __forceinline__ KvCursor kv_next(const ChunkTable& ct, int64_t kvo, c
 // writes per MFMA against two 4-wave blocks per CU.
 constexpr int kFwdWaves = 8;
 constexpr int kFwdRows = 32 * kFwdWaves;
+static_assert(kFwdRows == kQueryBlockRows, "the host sizes KV splits with kQueryBlockRows");
 // Keys per tile = 64 * kFwdSub: fewer barriers, pipeline fills and row-max
 // passes per key; the block's LDS holds two such K / V tiles.
 constexpr int kFwdSub = 2;
@@ -435,6 +450,7 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
   const int l32 = lane & 31, g = lane >> 5;
   int qt, h, b;
   decode_block((p.T + kFwdRows - 1) / kFwdRows, p.H, qt, h, b);
+  const KvSplit sp = kv_split(p.ct.n);
   const int qi = qt * kFwdRows + wave * 32 + l32;
   const bool q_ok = qi < p.T;
   const float c2 = p.scale * kLog2e;
@@ -489,18 +505,18 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
     else vld.load_one(nv_rs[sb], Vs[bf][sb], k - kSlotsK);
   };
   KvCursor cur;
-  kv_enter(p.ct, kvo, 0, cur);
+  kv_enter(p.ct, kvo, sp.begin, sp.end, cur);
   int buf = 0;
-  if (cur.step < p.ct.n) issue(cur, 0);
+  if (cur.step < sp.end) issue(cur, 0);
 #pragma unroll
   for (int ks = 0; ks < KSTEPS; ++ks) settle(qf[ks]);
 #pragma unroll 1
-  while (cur.step < p.ct.n) {
+  while (cur.step < sp.end) {
     const int kv_left = cur.len - cur.k0;
-    const KvCursor nxt = kv_next(p.ct, kvo, cur, 64 * NS);
+    const KvCursor nxt = kv_next(p.ct, kvo, cur, 64 * NS, sp.end);
     wait_lds_loads();
     __syncthreads();
-    const bool has_next = nxt.step < p.ct.n;
+    const bool has_next = nxt.step < sp.end;
     if (has_next) {
 #pragma unroll
       for (int sb = 0; sb < NS; ++sb) {
@@ -590,7 +606,7 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
   const int lane_e = lane_id_fresh(), g_e = lane_e >> 5;
   const int qi_e = qt * kFwdRows + wave * 32 + (lane_e & 31);
   if (qi_e >= p.T) return;
-  float* orow = p.out + (int64_t)b * p.sob + (int64_t)h * p.soh + (int64_t)qi_e * p.sot;
+  float* orow = p.out + sp.index * p.split_o + (int64_t)b * p.sob + (int64_t)h * p.soh + (int64_t)qi_e * p.sot;
 #pragma unroll
   for (int db = 0; db < DBLK; ++db)
 #pragma unroll
@@ -599,7 +615,7 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
       if (d < p.D) orow[d] = o[db][r] * inv;
     }
   if (g_e == 0) {
-    const int64_t si = ((int64_t)b * p.H + h) * p.T + qi_e;
+    const int64_t si = sp.index * p.split_ml + ((int64_t)b * p.H + h) * p.T + qi_e;
     const float m_nat = m_max * kLn2;
     if (p.m_bf16) {
       const bf16 mh = (bf16)m_nat;
@@ -662,6 +678,7 @@ __global__ __launch_bounds__(256) void stats_prep_kernel(BwdParams p) {
 // the same reason as the forward: each K / V tile in LDS serves 256 queries.
 constexpr int kDqWaves = 8;
 constexpr int kDqRows = 32 * kDqWaves;
+static_assert(kDqRows == kQueryBlockRows, "the host sizes KV splits with kQueryBlockRows");
 // Keys per barrier interval = 64 * kDqSub (kDqSub 64-row LDS sub-tiles per
 // buffer).  Within an interval the 32-key blocks j = 0 .. 2*kDqSub-1 run as
 // one software pipeline: A(j) = S^T, dP^T of block j; B(j) = its dS^T (VALU);
@@ -689,6 +706,7 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
   const int l32 = lane & 31, g = lane >> 5;
   int qt, h, b;
   decode_block((p.T + kDqRows - 1) / kDqRows, p.H, qt, h, b);
+  const KvSplit sp = kv_split(p.ct.n);
   const int qi = qt * kDqRows + wave * 32 + l32;
   const bool q_ok = qi < p.T;
   const float c2 = p.scale * kLog2e;
@@ -757,9 +775,9 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
     else vld.load_one(nv_rs[sb], Vs[bf][sb], k - kSlotsK);
   };
   KvCursor cur;
-  kv_enter(p.ct, kvo, 0, cur);
+  kv_enter(p.ct, kvo, sp.begin, sp.end, cur);
   int buf = 0;
-  if (cur.step < p.ct.n) issue(cur, 0);
+  if (cur.step < sp.end) issue(cur, 0);
 #pragma unroll
   for (int ks = 0; ks < KSTEPS; ++ks) {
     settle(qf[ks]);
@@ -769,11 +787,11 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
   settle(lse2_s);
   settle(dlt_s);
 #pragma unroll 1
-  while (cur.step < p.ct.n) {
-    const KvCursor nxt = kv_next(p.ct, kvo, cur, 64 * NS);
+  while (cur.step < sp.end) {
+    const KvCursor nxt = kv_next(p.ct, kvo, cur, 64 * NS, sp.end);
     wait_lds_loads();
     __syncthreads();
-    const bool has_next = nxt.step < p.ct.n;
+    const bool has_next = nxt.step < sp.end;
     if (has_next) prepare(nxt);
 
     // S^T / dP^T of two 32-key blocks in flight (block j in slot j & 1) and
@@ -851,7 +869,8 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
   const int lane_e = lane_id_fresh(), g_e = lane_e >> 5;  // as in the forward's epilogue
   const int qi_e = qt * kDqRows + wave * 32 + (lane_e & 31);
   if (qi_e >= p.T) return;
-  char* drow = (char*)p.dq + (((int64_t)b * p.sdqb + (int64_t)h * p.sdqh + (int64_t)qi_e * p.sdqt) << (p.dq_f32 ? 2 : 1));
+  char* drow = (char*)p.dq + ((sp.index * p.split_dq + (int64_t)b * p.sdqb + (int64_t)h * p.sdqh +
+                               (int64_t)qi_e * p.sdqt) << (p.dq_f32 ? 2 : 1));
 #pragma unroll
   for (int db = 0; db < DBLK; ++db)
 #pragma unroll
@@ -1094,6 +1113,87 @@ __global__ __launch_bounds__(64 * kDkWaves, 1) void dkdv_kernel(BwdParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// KV-split merges: 16 lanes per query row, 8 elements of D per lane
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void fwd_merge_kernel(FwdMergeParams p) {
+  const int64_t rows = (int64_t)p.B * p.H * p.T;
+  const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int sub = threadIdx.x & 15, d0 = sub * 8;
+  if (row >= rows) return;  // whole 16-lane groups
+  float mx = -INFINITY;
+  for (int s = 0; s < p.n_split; ++s) mx = fmaxf(mx, p.part_m[s * rows + row]);
+  float l = 0.f, acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+  for (int s = 0; s < p.n_split; ++s) {
+    const float ls = p.part_l[s * rows + row];
+    // a split without keys (l = 0) adds nothing; NaN statistics propagate
+    const float w = (ls == 0.f) ? 0.f : ls * __expf(p.part_m[s * rows + row] - mx);
+    l += w;
+    if (w != 0.f && d0 < p.D) {
+      const float* o = p.part_o + (s * rows + row) * p.D + d0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] += w * o[j];
+    }
+  }
+  const int t = (int)(row % p.T);
+  const int64_t bh = row / p.T;
+  const int h = (int)(bh % p.H), b = (int)(bh / p.H);
+  const float inv = (l > 0.f) ? 1.f / l : 0.f;
+  if (d0 < p.D) {
+    float* orow = p.out + (int64_t)b * p.sob + (int64_t)h * p.soh + (int64_t)t * p.sot + d0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) orow[j] = acc[j] * inv;
+  }
+  if (sub == 0) {  // statistics as the forward kernel writes them
+    if (p.m_bf16) {
+      const bf16 mh = (bf16)mx;
+      const float mhf = (float)mh;
+      ((bf16*)p.m)[row] = mh;
+      p.l[row] = (l > 0.f) ? l * __expf(mx - mhf) : 0.f;
+    } else {
+      ((float*)p.m)[row] = mx;
+      p.l[row] = l;
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void dq_merge_kernel(DqMergeParams p) {
+  const int64_t rows = (int64_t)p.B * p.H * p.T;
+  const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int d0 = (threadIdx.x & 15) * 8;
+  if (row >= rows || d0 >= p.D) return;
+  float acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+  for (int s = 0; s < p.n_split; ++s) {
+    const float* o = p.part + (s * rows + row) * p.D + d0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] += o[j];
+  }
+  const int t = (int)(row % p.T);
+  const int64_t bh = row / p.T;
+  const int h = (int)(bh % p.H), b = (int)(bh / p.H);
+  const int64_t e = (int64_t)b * p.sdqb + (int64_t)h * p.sdqh + (int64_t)t * p.sdqt + d0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    if (p.dq_f32) ((float*)p.dq)[e + j] = acc[j];
+    else ((bf16*)p.dq)[e + j] = (bf16)acc[j];
+  }
+}
+
+hipError_t launch_fwd_merge(const FwdMergeParams& p, hipStream_t st) {
+  const int64_t rows = (int64_t)p.B * p.H * p.T;
+  hipLaunchKernelGGL(fwd_merge_kernel, dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, st, p);
+  return hipGetLastError();
+}
+hipError_t launch_dq_merge(const DqMergeParams& p, hipStream_t st) {
+  const int64_t rows = (int64_t)p.B * p.H * p.T;
+  hipLaunchKernelGGL(dq_merge_kernel, dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, st, p);
+  return hipGetLastError();
+}
+
 hipError_t launch_stats_prep(const BwdParams& p, hipStream_t st) {
   const int64_t n = (int64_t)p.B * p.H * p.T;
   hipLaunchKernelGGL(stats_prep_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, p);
@@ -1120,13 +1220,13 @@ HARP_RA_INSTANTIATE(8, 4)
 template <int KSTEPS, int DBLK>
 static hipError_t launch_fwd_t(const FwdParams& p, hipStream_t st) {
   const int n = ((p.T + kFwdRows - 1) / kFwdRows) * p.H * p.B;
-  hipLaunchKernelGGL((fwd_kernel<KSTEPS, DBLK>), dim3(n), dim3(64 * kFwdWaves), 0, st, p);
+  hipLaunchKernelGGL((fwd_kernel<KSTEPS, DBLK>), dim3(n, p.n_split), dim3(64 * kFwdWaves), 0, st, p);
   return hipGetLastError();
 }
 template <int KSTEPS, int DBLK>
 static hipError_t launch_dq_t(const BwdParams& p, hipStream_t st) {
   const int n = ((p.T + kDqRows - 1) / kDqRows) * p.H * p.B;
-  hipLaunchKernelGGL((dq_kernel<KSTEPS, DBLK>), dim3(n), dim3(64 * kDqWaves), 0, st, p);
+  hipLaunchKernelGGL((dq_kernel<KSTEPS, DBLK>), dim3(n, p.n_split), dim3(64 * kDqWaves), 0, st, p);
   return hipGetLastError();
 }
 template <int KSTEPS, int DBLK>

@@ -166,7 +166,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> forward_hip(const at::Tensor& q, 
   const c10::DeviceGuard guard(q.device());
   const int B = q.size(0), H = q.size(1), T = q.size(2), D = q.size(3);
   const int32_t* lens = ch.lens.empty() ? nullptr : ch.lens.data();
-  const size_t ws_bytes = harp_ra_forward_workspace_bytes(B, H, D, sp_size, ch.chunk_len, lens);
+  const size_t ws_bytes = harp_ra_forward_workspace_bytes(B, H, T, D, sp_size, ch.chunk_len, lens);
   check_status(ws_bytes != SIZE_MAX ? HARP_RA_OK : HARP_RA_EINVAL, "ring_attention_forward");
   at::Tensor ws = workspace(ws_bytes, q);
   const auto qs = strides4(q), ks = strides4(k), os = strides4(out);

@@ -108,16 +108,18 @@ def _lens_arg(kv_lens):
 _SIZE_MAX = 2**64 - 1
 
 
-def forward_workspace_bytes(B, H, D, sp_size, chunk_len, kv_lens=None) -> int:
-    """Device scratch bytes the forward needs (raises on invalid sizes)."""
-    n = int(_lib.load_abi().harp_ra_forward_workspace_bytes(B, H, D, sp_size, chunk_len, _lens_arg(kv_lens)))
+def forward_workspace_bytes(B, H, T, D, sp_size, chunk_len, kv_lens=None) -> int:
+    """Device scratch bytes the forward needs on the current device (raises
+    on invalid sizes)."""
+    n = int(_lib.load_abi().harp_ra_forward_workspace_bytes(B, H, T, D, sp_size, chunk_len, _lens_arg(kv_lens)))
     if n == _SIZE_MAX:
         raise ValueError(_lib.last_error())
     return n
 
 
 def backward_workspace_bytes(B, H, T, D, sp_size, chunk_len, kv_lens=None) -> int:
-    """Device scratch bytes the backward needs (raises on invalid sizes)."""
+    """Device scratch bytes the backward needs on the current device (raises
+    on invalid sizes)."""
     n = int(_lib.load_abi().harp_ra_backward_workspace_bytes(B, H, T, D, sp_size, chunk_len, _lens_arg(kv_lens)))
     if n == _SIZE_MAX:
         raise ValueError(_lib.last_error())
@@ -150,7 +152,7 @@ def abi_forward(
     n = len(k_chunks)
     chunk_len = k_chunks[0].shape[2]
     if workspace is None:
-        workspace = _workspace(forward_workspace_bytes(B, H, D, n, chunk_len, kv_lens), q.device)
+        workspace = _workspace(forward_workspace_bytes(B, H, T, D, n, chunk_len, kv_lens), q.device)
     m_code = _lib.HARP_RA_BF16 if m_i.dtype == torch.bfloat16 else _lib.HARP_RA_F32
     rc = lib.harp_ra_forward(
         q.data_ptr(), _strides(q),

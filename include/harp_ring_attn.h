@@ -113,15 +113,21 @@ HARP_RA_API int harp_ra_delta(const void* grad_out, const int64_t* do_strides,
                   int batch, int h_num, int t_num, int h_len, void* stream);
 
 /*
- * Device workspace the forward / backward need for these sizes ((size_t)-1
- * when the arguments are invalid; 0 = none needed).  The forward keeps all
- * staging in LDS and needs none; the backward needs 8 bytes per query row
- * (B*H*T, rounded up to 256 bytes) for its per-query statistics, prepared
- * once per call.  Replaces the reference's grow-only scratch sizing
+ * Device workspace the forward / backward need for these sizes on the
+ * current device ((size_t)-1 when the arguments are invalid; 0 = none
+ * needed).  The forward keeps all staging in LDS; the backward needs 8 bytes
+ * per query row (B*H*T, rounded up to 256 bytes) for its per-query
+ * statistics, prepared once per call.  When the forward / dQ grids would
+ * leave at least half of the device's compute units idle (fewer than
+ * CUs / 2 tiles of 256 queries over B and H) and there are several chunks,
+ * the ring steps are split over up to sp_size blocks per tile: the forward
+ * then needs n * B*H*T * (4*h_len + 8) bytes for the splits' partial O, m
+ * and l, and the backward n * B*H*T * 4*h_len more for the dQ partials (each
+ * part rounded up to 256 bytes).  Replaces the reference's grow-only scratch sizing
  * (RingAttnHbmWorkspace::ensure_slot, ring_attn.cpp:620-840, sized at
  * :2428-2450 and :2595-2656).
  */
-HARP_RA_API size_t harp_ra_forward_workspace_bytes(int batch, int h_num, int h_len, int sp_size,
+HARP_RA_API size_t harp_ra_forward_workspace_bytes(int batch, int h_num, int t_num, int h_len, int sp_size,
                                        int kv_chunk_len, const int32_t* kv_valid_lens);
 HARP_RA_API size_t harp_ra_backward_workspace_bytes(int batch, int h_num, int t_num, int h_len,
                                         int sp_size, int kv_chunk_len,

@@ -95,14 +95,15 @@ def test_forward_rejects_bad_arguments_before_any_device_call(over, code, msg):
 def test_workspace_sizes():
     # the forward stages everything in LDS; the backward keeps two fp32
     # statistics planes of B*H*T rows, rounded up to 256 bytes
-    assert harp_amd.forward_workspace_bytes(1, 24, 128, 8, 8192) == 0
+    # (no device here: KV splits, which depend on the device's CU count, are off)
+    assert harp_amd.forward_workspace_bytes(1, 24, 8192, 128, 8, 8192) == 0
     assert harp_amd.backward_workspace_bytes(1, 24, 8192, 128, 8, 8192) == 2 * 4 * 24 * 8192
     assert harp_amd.backward_workspace_bytes(1, 1, 33, 64, 1, 64) == 512
-    assert harp_amd.forward_workspace_bytes(2, 16, 72, 4, 4480, [4429] * 4) == 0
+    assert harp_amd.forward_workspace_bytes(2, 16, 4429, 72, 4, 4480, [4429] * 4) == 0
     with pytest.raises(ValueError, match="sp_size"):
-        harp_amd.forward_workspace_bytes(1, 1, 64, 0, 64)
+        harp_amd.forward_workspace_bytes(1, 1, 64, 64, 0, 64)
     with pytest.raises(ValueError, match="multiple of 8"):
-        harp_amd.forward_workspace_bytes(1, 1, 66, 1, 64)
+        harp_amd.forward_workspace_bytes(1, 1, 64, 66, 1, 64)
 
 
 def test_timing_read_validates_arguments():
