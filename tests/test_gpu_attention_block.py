@@ -122,6 +122,49 @@ def test_block_matches_fp64_reference(qk_norm, rope):
     assert max(v for k, v in errs.items() if k != "out") <= 3e-2, errs
 
 
+def test_block_at_model_width():
+    """The model's own width (standalone_transformer.py:423-440: dim 3840,
+    30 heads x 128) over a 2048-token sequence in 2 ring chunks, with norm and
+    RoPE; the fp64 reference runs on the GPU."""
+    B, S, dim, heads, D, sp = 1, 2048, 3840, 30, 128, 2
+    eps = 1e-5
+    torch.manual_seed(30)
+    attn = _Attn(dim, heads, D, True, eps)
+    with torch.no_grad():
+        for mod in (attn.norm_q, attn.norm_k):
+            mod.weight.copy_(1 + 0.2 * torch.randn(D))
+    attn = attn.to(torch.bfloat16)
+    x = torch.randn(B, S, dim).to(torch.bfloat16)
+    dy = torch.randn(B, S, dim).to(torch.bfloat16)
+    ang = torch.arange(S, dtype=torch.float64)[:, None] * (10000.0 ** (-2.0 * torch.arange(D // 2) / D))[None, :]
+    freqs = torch.polar(torch.ones_like(ang), ang)
+
+    gattn = _Attn(dim, heads, D, True, eps).to(torch.bfloat16)
+    gattn.load_state_dict(attn.state_dict())
+    gattn = gattn.to(DEV)
+    xg = x.to(DEV).requires_grad_(True)
+    yg = harp_amd.RingZAttention(gattn, sp)(xg, freqs.to(torch.complex64).to(DEV))
+    yg.backward(dy.to(DEV))
+
+    p = {n: t.detach().to(DEV).double().requires_grad_(True) for n, t in attn.state_dict().items()
+         if n in _params(attn)}
+    xr = x.to(DEV).double().requires_grad_(True)
+    yr = _reference(p, xr, freqs.to(DEV), heads, eps, True)
+    yr.backward(dy.to(DEV).double())
+    torch.cuda.synchronize()
+
+    def rel(a, b):
+        return ((a.detach().double() - b.detach()).norm() / b.detach().norm()).item()
+
+    errs = {"out": rel(yg, yr), "d_hidden": rel(xg.grad, xr.grad)}
+    gparams = dict(gattn.named_parameters())
+    for n in _params(attn):
+        errs["d_" + n] = rel(gparams[n].grad, p[n].grad)
+    print({k: f"{v:.2e}" for k, v in errs.items()}, flush=True)
+    assert errs["out"] <= 2e-2, errs
+    assert max(v for k, v in errs.items() if k != "out") <= 3e-2, errs
+
+
 def test_block_rejects_a_sequence_not_split_into_chunks():
     attn = _Attn(64, 1, 64, True).to(torch.bfloat16).to(DEV)
     with pytest.raises(ValueError, match="multiple of sp_size"):

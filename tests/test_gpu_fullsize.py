@@ -1,0 +1,94 @@
+"""Full-size GPU parity of the ring-attention operators at BASELINE configs
+3, 4 and 5: every output element (O, LSE and delta of every row, dQ, dK and
+dV of every row) against the fp32 PyTorch reference of tests/gpu_reference.py
+run on the GPU on the same bf16 inputs.  The reference itself is pinned
+first against the CPU oracle (fp64) on small ragged problems.  Bars as the
+other parity tests: O, LSE, delta <= 2e-2; dQ, dK, dV <= 3e-2 relative
+Frobenius error; pad keys' dK / dV exactly 0."""
+
+import math
+
+import pytest
+import torch
+
+from oracle import ring_attn_oracle as orc
+from tests.gpu_harness import run_hip
+from tests.gpu_reference import attention_fp32
+from tests.parity import TOL_GRAD, TOL_LSE, TOL_O, rel_fro
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(x):
+    return x.transpose(1, 2).contiguous().cuda().transpose(1, 2)
+
+
+@pytest.mark.parametrize("B,H,T,D,N,tc,lens", [
+    (1, 3, 150, 64, 3, 97, [97, 40, 0]),
+    (2, 2, 77, 72, 2, 130, [130, 129]),
+    (1, 2, 64, 128, 1, 300, None),
+])
+def test_reference_matches_oracle(B, H, T, D, N, tc, lens):
+    """The GPU fp32 reference agrees with the fp64 CPU oracle to fp32
+    precision, so it can stand in for it at sizes the oracle cannot reach."""
+    q, ks, vs, do = orc.make_inputs(B, H, T, D, N, seed=T + D, chunk_len=tc)
+    scale = 1.0 / math.sqrt(D)
+    ref = attention_fp32(_dev(q), [_dev(k) for k in ks], [_dev(v) for v in vs], _dev(do), scale, lens=lens,
+                         key_block=64)
+    for h in range(H):
+        sl = slice(h, h + 1)
+        o, m, l = orc.ring_forward(q[:, sl], [k[:, sl] for k in ks], [v[:, sl] for v in vs], scale,
+                                   kv_valid_lens=lens, dtype=torch.float64)
+        dl = orc.delta(do[:, sl], o, dtype=torch.float64)
+        dq, dks, dvs = orc.ring_backward(q[:, sl], [k[:, sl] for k in ks], [v[:, sl] for v in vs], do[:, sl], m, l,
+                                         dl, scale, kv_valid_lens=lens, dtype=torch.float64)
+        want = {"o": o, "lse": orc.lse_from_ml(m, l), "delta": dl, "dq": dq, "dk": torch.cat(dks, 2),
+                "dv": torch.cat(dvs, 2)}
+        for name, w in want.items():
+            got = ref[name][:, sl].double().cpu()
+            err = rel_fro(got, w)
+            assert err <= 1e-5, (name, h, err)
+
+
+def _inputs(B, H, T, D, N, tc, vscale, seed=3407):
+    """The benchmark's draw order (Q, K chunks, V chunks, dO), token-major on the device."""
+    g = torch.Generator().manual_seed(seed)
+
+    def draw(rows):
+        x = torch.randn((B, rows, H, D), generator=g) * vscale
+        return x.to(torch.bfloat16).cuda().transpose(1, 2)
+
+    q = draw(T)
+    ks = [draw(tc) for _ in range(N)]
+    vs = [draw(tc) for _ in range(N)]
+    do = draw(T)
+    return q, ks, vs, do
+
+
+@pytest.mark.parametrize("config,B,H,T,D,N,tc,lens,vscale", [
+    (3, 2, 16, 4096, 72, 8, 4096, None, 0.5),
+    (4, 1, 24, 8192, 128, 8, 8192, None, 1.0),
+    (5, 1, 24, 4429, 128, 4, 4480, [4429] * 4, 1.0),
+])
+def test_full_size_against_fp32_reference(config, B, H, T, D, N, tc, lens, vscale):
+    print(f"[config {config} full size]", flush=True)
+    q, ks, vs, do = _inputs(B, H, T, D, N, tc, vscale)
+    scale = 1.0 / math.sqrt(D)
+    res = run_hip(q.cpu(), [k.cpu() for k in ks], [v.cpu() for v in vs], do.cpu(), scale, kv_lens=lens,
+                  via="ops")
+    ref = attention_fp32(q, ks, vs, do, scale, lens=lens)
+    torch.cuda.synchronize()
+    tol = {"o": TOL_O, "lse": TOL_LSE, "delta": TOL_O, "dq": TOL_GRAD, "dk": TOL_GRAD, "dv": TOL_GRAD}
+    errs = {}
+    for name in tol:
+        got = res[name].cuda().double()
+        want = ref[name].double()
+        if name in ("dk", "dv") and lens is not None:
+            valid = torch.cat([torch.arange(tc) < n for n in lens]).cuda()
+            assert bool((got[:, :, ~valid] == 0).all()), f"{name}: pad keys must get 0"
+            got, want = got[:, :, valid], want[:, :, valid]
+        errs[name] = (torch.linalg.vector_norm(got - want) / torch.linalg.vector_norm(want)).item()
+        del got, want
+    print({k: f"{v:.2e}" for k, v in errs.items()}, flush=True)
+    for name, e in errs.items():
+        assert e <= tol[name], (name, e)
