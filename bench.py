@@ -413,6 +413,10 @@ def main() -> int:
     # sustained MFMA rate of this board (register-fed bf16 MFMA stream on
     # random operands): what the power limit lets any MFMA-bound kernel reach
     probe_tf, probe_ghz = _lib.probe_mfma_rate(4096, args.seed)
+    # the same at the kernels' operand path: one operand of every MFMA from
+    # LDS (1 KB per MFMA per wave, 8 waves per CU); the LDS reads draw power
+    # from the MFMA stream, so this is the ceiling for this kernel design
+    lds_tf, lds_ghz = _lib.probe_mfma_lds_rate(False, 32768, args.seed)
     kernels = {}
     for name, (ms, n) in kt.items():
         if n:
@@ -423,6 +427,7 @@ def main() -> int:
                 performed = kernel_mfma[name] / (avg * 1e-3) / 1e12
                 entry["tflops_mfma_performed"] = round(performed, 1)
                 entry["frac_of_sustained"] = round(performed / probe_tf, 4) if probe_tf > 0 else None
+                entry["frac_of_lds_fed"] = round(performed / lds_tf, 4) if lds_tf > 0 else None
             kernels[name] = entry
     dom = max((n for n in kernel_flops if n in kernels), key=lambda n: kt[n][0])
     dom_tf = kernels[dom]["tflops_algorithmic"]
@@ -464,6 +469,9 @@ def main() -> int:
             "sustained_mfma_tflops": round(probe_tf, 1),
             "sustained_mfma_shader_ghz": round(probe_ghz, 3),
             "frac_of_sustained": round(dom_tf / probe_tf, 4) if probe_tf > 0 else None,
+            "lds_fed_mfma_tflops": round(lds_tf, 1),
+            "lds_fed_mfma_shader_ghz": round(lds_ghz, 3),
+            "frac_of_lds_fed": round(dom_tf / lds_tf, 4) if lds_tf > 0 else None,
         },
         "cpu_baseline": None,
         "gpu": torch.cuda.get_device_name(0),

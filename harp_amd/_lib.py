@@ -175,6 +175,9 @@ def load_probe() -> ctypes.CDLL:
             lib.harp_probe_mfma_rate.restype = _i
             lib.harp_probe_mfma_rate.argtypes = [_i, ctypes.c_uint32, ctypes.POINTER(ctypes.c_double),
                                                  ctypes.POINTER(ctypes.c_double)]
+            lib.harp_probe_mfma_lds_rate.restype = _i
+            lib.harp_probe_mfma_lds_rate.argtypes = [_i, ctypes.c_uint32, _i, ctypes.POINTER(ctypes.c_double),
+                                                     ctypes.POINTER(ctypes.c_double)]
             lib.harp_probe_last_error.restype = ctypes.c_char_p
             lib.harp_probe_last_error.argtypes = []
             _probe = lib
@@ -190,6 +193,21 @@ def probe_mfma_rate(iters: int = 4096, seed: int = 3407) -> tuple:
     rc = lib.harp_probe_mfma_rate(int(iters), int(seed) & 0xFFFFFFFF, ctypes.byref(tf), ctypes.byref(ghz))
     if rc != 0:
         raise RuntimeError(f"harp_probe_mfma_rate failed (status {rc}): {lib.harp_probe_last_error().decode()}")
+    return tf.value, ghz.value
+
+
+def probe_mfma_lds_rate(softmax: bool, iters: int = 8192, seed: int = 3407) -> tuple:
+    """(TFLOP/s, shader GHz) of the same MFMA stream at the attention kernels'
+    occupancy (8 waves per CU) with one operand of every MFMA read from LDS
+    (1 KB per MFMA per wave), and with softmax=True one exp and three FMAs per
+    MFMA besides: the rate that operand path allows under the power limit."""
+    lib = load_probe()
+    tf = ctypes.c_double()
+    ghz = ctypes.c_double()
+    rc = lib.harp_probe_mfma_lds_rate(int(iters), int(seed) & 0xFFFFFFFF, 1 if softmax else 0, ctypes.byref(tf),
+                                      ctypes.byref(ghz))
+    if rc != 0:
+        raise RuntimeError(f"harp_probe_mfma_lds_rate failed (status {rc}): {lib.harp_probe_last_error().decode()}")
     return tf.value, ghz.value
 
 

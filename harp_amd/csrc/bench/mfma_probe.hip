@@ -1,15 +1,24 @@
 // Bench-only device probe (kernels/libharp_probe.so, loaded by bench.py; not
 // part of the drop-in libraries): the sustained dense bf16 MFMA rate of this
-// GPU and the shader clock it runs at while doing only that.
+// GPU, and the shader clock it runs at, for three instruction mixes.
 //
-// Every wave streams v_mfma_f32_32x32x16_bf16 (the instruction all ring-
-// attention kernels use) from registers: four independent accumulator
-// chains, operands drawn from a per-lane hash of the seed (bf16 values in
-// [-1, 1), so the multiplier inputs toggle like real data; all-zero operands
-// draw far less power and run at a higher clock).  No LDS, no global traffic
-// inside the loop.  The result bounds what any MFMA-bound kernel can reach on
-// this board under its power limit, independently of the published peak
-// (256 CU x 2.4 GHz x 4096 FLOP/clk).
+// 1. harp_probe_mfma_rate: every wave streams v_mfma_f32_32x32x16_bf16 (the
+//    instruction all ring-attention kernels use) from registers: four
+//    independent accumulator chains, operands drawn from a per-lane hash of
+//    the seed (bf16 values in [-1, 1), so the multiplier inputs toggle like
+//    real data; all-zero operands draw far less power and run at a higher
+//    clock).  32 waves per CU.  No LDS, no global traffic inside the loop.
+// 2. harp_probe_mfma_lds_rate(softmax = 0): the attention kernels' operand
+//    path -- 8 waves per CU (two per SIMD, as the kernels run), and one
+//    operand of every MFMA read from LDS by ds_read_b128, 1 KB per MFMA per
+//    wave (a 32x16 bf16 fragment), issued one MFMA ahead of its use.  The
+//    other operand stays in registers, as Q, dO or P do in the kernels.
+// 3. harp_probe_mfma_lds_rate(softmax = 1): the same plus one v_exp_f32 and
+//    three FMAs per MFMA, the forward kernel's per-MFMA softmax work.
+// The board is power-limited under MFMA load: LDS reads and VALU work take
+// power from the MFMA stream, so mixes 2 and 3 run at a lower clock than 1.
+// They bound what a kernel with that operand path can reach, independently
+// of the published peak (256 CU x 2.4 GHz x 4096 FLOP/clk).
 //
 // Clock: each block's first wave reads the shader-clock counter (s_memtime)
 // and the constant-rate counter (s_memrealtime) around its loop; the average
@@ -17,6 +26,7 @@
 //
 // C ABI (ctypes in harp_amd/_lib.py):
 //   int harp_probe_mfma_rate(int iters, uint32_t seed, double* tflops, double* shader_ghz);
+//   int harp_probe_mfma_lds_rate(int iters, uint32_t seed, int softmax, double* tflops, double* shader_ghz);
 //   const char* harp_probe_last_error(void);
 // Status 0 = ok, 1 = bad argument, 3 = allocation failed, 4 = launch failed.
 // Synchronous on the null stream; allocates and frees its own small buffers.
@@ -94,6 +104,72 @@ __global__ __launch_bounds__(256) void mfma_probe_kernel(uint32_t seed, int iter
   }
 }
 
+// Mixes 2 and 3: 8 waves, 64 KB of random bf16 in LDS.  The LDS reads and the
+// MFMAs that consume the previous step's fragments are one asm block, so the
+// compiler cannot sink the reads down to their use (which would expose their
+// latency) and the reads of step i + 1 overlap the MFMAs of step i.  Every
+// address is lane * 16 + group * 4096 + k * 1024 + 16 bytes <= 65536.
+constexpr int kLdsProbeWaves = 8;
+constexpr int kLdsProbeFrags = 64 * 64;  // bf16x8 fragments, 64 KB
+
+template <bool SOFTMAX>
+__global__ __launch_bounds__(64 * kLdsProbeWaves) void mfma_lds_probe_kernel(uint32_t seed, int iters, float* sink,
+                                                                            long long* clocks) {
+  __shared__ __attribute__((aligned(16))) bf16x8 lds[kLdsProbeFrags];
+  const uint32_t gid = blockIdx.x * (64u * kLdsProbeWaves) + threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  for (int i = threadIdx.x; i < kLdsProbeFrags; i += 64 * kLdsProbeWaves)
+    lds[i] = random_bf16x8(hash32(seed + 7u) ^ (blockIdx.x * (uint32_t)kLdsProbeFrags + (uint32_t)i));
+  __syncthreads();
+  bf16x8 b[4], x[2][4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    b[j] = random_bf16x8(hash32(seed + 1u) ^ (gid * 8u + 4u + (uint32_t)j));
+    x[0][j] = lds[j * 64 + lane];
+    x[1][j] = x[0][j];
+  }
+  float e[4] = {-0.01f * (float)lane, -0.5f, -0.25f, -1.f};
+  const uint32_t base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)&lds[lane];
+  f32x16 c0 = zero16(), c1 = zero16(), c2 = zero16(), c3 = zero16();
+  auto step = [&](const bf16x8* u, bf16x8* w, uint32_t addr) {
+    asm volatile(
+        "ds_read_b128 %4, %16 offset:0\n\t"
+        "v_mfma_f32_32x32x16_bf16 %0, %8, %12, %0\n\t"
+        "ds_read_b128 %5, %16 offset:1024\n\t"
+        "v_mfma_f32_32x32x16_bf16 %1, %9, %13, %1\n\t"
+        "ds_read_b128 %6, %16 offset:2048\n\t"
+        "v_mfma_f32_32x32x16_bf16 %2, %10, %14, %2\n\t"
+        "ds_read_b128 %7, %16 offset:3072\n\t"
+        "v_mfma_f32_32x32x16_bf16 %3, %11, %15, %3\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "+v"(c0), "+v"(c1), "+v"(c2), "+v"(c3), "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3])
+        : "v"(u[0]), "v"(u[1]), "v"(u[2]), "v"(u[3]), "v"(b[0]), "v"(b[1]), "v"(b[2]), "v"(b[3]), "v"(addr));
+    if (SOFTMAX) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float t = __builtin_amdgcn_exp2f(e[k]);
+        e[k] = __builtin_fmaf(t, -0.001f, e[k]);
+        e[k] = __builtin_fmaf(e[k], 0.999f, -0.0001f);
+        e[k] = __builtin_fmaf(e[k], 1.0001f, 0.00001f);
+      }
+    }
+  };
+  const long long t0 = clock64(), r0 = wall_clock64();
+  for (int i = 0; i < iters; i += 2) {
+    step(x[0], x[1], base + (uint32_t)(((i + 1) & 15) * 4096));
+    step(x[1], x[0], base + (uint32_t)(((i + 2) & 15) * 4096));
+  }
+  const long long t1 = clock64(), r1 = wall_clock64();
+  float s = e[0] + e[1] + e[2] + e[3];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) s += c0[j] + c1[j] + c2[j] + c3[j];
+  sink[gid] = s;
+  if (threadIdx.x == 0) {
+    clocks[2 * blockIdx.x] = t1 - t0;
+    clocks[2 * blockIdx.x + 1] = r1 - r0;
+  }
+}
+
 thread_local std::string g_last_error;
 
 int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
@@ -116,28 +192,25 @@ int launched(const char* what) {
   return kOk;
 }
 
-}  // namespace
-
-extern "C" {
-
-__attribute__((visibility("default"))) const char* harp_probe_last_error(void) { return g_last_error.c_str(); }
-
-__attribute__((visibility("default"))) int harp_probe_mfma_rate(int iters, uint32_t seed, double* tflops,
-                                                                double* shader_ghz) {
+// mix 0: register-fed, 32 waves per CU; mix 1 / 2: LDS-fed (without / with
+// the softmax VALU), 8 waves per CU
+int run_probe(int mix, int iters, uint32_t seed, double* tflops, double* shader_ghz) {
   if (!tflops || !shader_ghz) return fail(kEinval, "probe outputs are NULL");
-  if (iters < 16 || iters > (1 << 20)) return fail(kEinval, "iters=%d must be in [16, 2^20]", iters);
+  if (iters < 16 || iters > (1 << 20) || iters % 2) return fail(kEinval, "iters=%d must be even, in [16, 2^20]", iters);
   int dev = 0, cus = 0, wall_khz = 0;
   if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) ||
       hipDeviceGetAttribute(&wall_khz, hipDeviceAttributeWallClockRate, dev) || cus < 1 || wall_khz < 1)
     return fail(kElaunch, "device query failed");
-  const int blocks = 8 * cus;  // 32 waves per CU, 8 per SIMD
+  const int threads = mix == 0 ? 256 : 64 * kLdsProbeWaves;
+  const int waves_per_block = threads / 64;
+  const int blocks = mix == 0 ? 8 * cus : cus;  // 32 or 8 waves per CU
   float* sink = nullptr;
   long long* clocks = nullptr;
   hipEvent_t e0 = nullptr, e1 = nullptr;
   int rc = kOk;
   std::vector<long long> h(2 * (size_t)blocks);
   float best_ms = 0.f;
-  if (hipMalloc(&sink, sizeof(float) * 256 * (size_t)blocks) != hipSuccess ||
+  if (hipMalloc(&sink, sizeof(float) * threads * (size_t)blocks) != hipSuccess ||
       hipMalloc(&clocks, sizeof(long long) * 2 * (size_t)blocks) != hipSuccess) {
     rc = fail(kEnomem, "probe buffers: hipMalloc failed");
   } else if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
@@ -146,8 +219,16 @@ __attribute__((visibility("default"))) int harp_probe_mfma_rate(int iters, uint3
     // one warm-up launch (clocks ramp), then the timed one
     for (int rep = 0; rep < 2 && rc == kOk; ++rep) {
       (void)hipEventRecord(e0, nullptr);
-      hipLaunchKernelGGL(mfma_probe_kernel, dim3((unsigned)blocks), dim3(256), 0, nullptr, seed + (uint32_t)rep, iters,
-                         sink, clocks);
+      const uint32_t sd = seed + (uint32_t)rep;
+      if (mix == 0)
+        hipLaunchKernelGGL(mfma_probe_kernel, dim3((unsigned)blocks), dim3(threads), 0, nullptr, sd, iters, sink,
+                           clocks);
+      else if (mix == 1)
+        hipLaunchKernelGGL(mfma_lds_probe_kernel<false>, dim3((unsigned)blocks), dim3(threads), 0, nullptr, sd, iters,
+                           sink, clocks);
+      else
+        hipLaunchKernelGGL(mfma_lds_probe_kernel<true>, dim3((unsigned)blocks), dim3(threads), 0, nullptr, sd, iters,
+                           sink, clocks);
       if ((rc = launched("MFMA probe"))) break;
       (void)hipEventRecord(e1, nullptr);
       if (hipEventSynchronize(e1) != hipSuccess || hipEventElapsedTime(&best_ms, e0, e1) != hipSuccess)
@@ -163,7 +244,7 @@ __attribute__((visibility("default"))) int harp_probe_mfma_rate(int iters, uint3
       shader += (double)h[2 * i];
       wall += (double)h[2 * i + 1];
     }
-    const double flop = (double)blocks * 4.0 /* waves */ * 4.0 * iters * 32.0 * 32.0 * 16.0 * 2.0;
+    const double flop = (double)blocks * waves_per_block * 4.0 * iters * 32.0 * 32.0 * 16.0 * 2.0;
     *tflops = (best_ms > 0.f) ? flop / (best_ms * 1e-3) / 1e12 : 0.0;
     *shader_ghz = (wall > 0.0) ? shader / wall * wall_khz * 1e-6 : 0.0;
   }
@@ -172,6 +253,23 @@ __attribute__((visibility("default"))) int harp_probe_mfma_rate(int iters, uint3
   if (sink) (void)hipFree(sink);
   if (clocks) (void)hipFree(clocks);
   return rc == kOk ? ok() : rc;
+}
+
+}  // namespace
+
+extern "C" {
+
+__attribute__((visibility("default"))) const char* harp_probe_last_error(void) { return g_last_error.c_str(); }
+
+__attribute__((visibility("default"))) int harp_probe_mfma_rate(int iters, uint32_t seed, double* tflops,
+                                                                double* shader_ghz) {
+  return run_probe(0, iters, seed, tflops, shader_ghz);
+}
+
+__attribute__((visibility("default"))) int harp_probe_mfma_lds_rate(int iters, uint32_t seed, int softmax,
+                                                                    double* tflops, double* shader_ghz) {
+  if (softmax != 0 && softmax != 1) return fail(kEinval, "softmax=%d must be 0 or 1", softmax);
+  return run_probe(1 + softmax, iters, seed, tflops, shader_ghz);
 }
 
 }  // extern "C"
