@@ -237,27 +237,8 @@ def producer_bench(cfg, seed: int, iters: int = 20):
     norm = SimpleNamespace(weight=w, eps=1e-6)
     attn = SimpleNamespace(heads=H, to_q=lin[0], to_k=lin[1], to_v=lin[2], norm_q=norm, norm_k=norm)
     hid = torch.randn((B, T, dim), generator=g).to(torch.bfloat16).to(dev)
-    with torch.no_grad():
-        for _ in range(3):
-            harp_amd.project_qkv(attn, hid, freqs)
-        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
-        torch.cuda.synchronize()
-        ev[0].record()
-        for _ in range(iters):
-            harp_amd.project_qkv(attn, hid, freqs)
-        ev[1].record()
-        torch.cuda.synchronize()
-    ms = ev[0].elapsed_time(ev[1]) / iters
     gemm_flop = 3 * 2 * B * T * dim * dim
-    res["project_qkv_forward"] = {
-        "avg_ms": round(ms, 4),
-        "gemm_flop": gemm_flop,
-        "tflops_incl_norm_rope": round(gemm_flop / (ms * 1e-3) / 1e12, 1),
-        "what": f"3 projections [{B},{T},{dim}] x [{dim},{dim}] (torch Linear, hipBLASLt) + fused norm+RoPE of q and k",
-    }
 
-    # the parts on their own, and the alternative of one GEMM over the
-    # concatenated q/k/v weights (N = 3 * dim) followed by the same passes
     def timed(fn, n=iters):
         for _ in range(3):
             fn()
@@ -269,6 +250,34 @@ def producer_bench(cfg, seed: int, iters: int = 20):
         e[1].record()
         torch.cuda.synchronize()
         return e[0].elapsed_time(e[1]) / n
+
+    # the producer as harp_amd.project_qkv runs it (fused kernel: projections
+    # with norm + RoPE in the epilogue), and the unfused path beside it
+    with torch.no_grad():
+        ms = timed(lambda: harp_amd.project_qkv(attn, hid, freqs))
+        ms_unfused = timed(lambda: harp_amd.project_qkv(attn, hid, freqs, fused=False))
+    res["project_qkv_forward"] = {
+        "avg_ms": round(ms, 4),
+        "gemm_flop": gemm_flop,
+        "tflops_incl_norm_rope": round(gemm_flop / (ms * 1e-3) / 1e12, 1),
+        "what": f"3 projections [{B},{T},{dim}] x [{dim},{dim}] with norm+RoPE of q and k in the epilogue "
+                "(one launch of the fused projection kernel)",
+        "unfused_avg_ms": round(ms_unfused, 4),
+        "unfused_what": "torch Linear (hipBLASLt) x 3, then the fused norm+RoPE kernel on q and k",
+    }
+    # the fused kernel alone, HIP events on the launch stream, and as the
+    # training forward runs it (pre-norm products and rms also written)
+    from harp_amd import qkv as _qkv
+
+    ws3 = [m.weight for m in lin]
+    nrm = [(w, 1e-6), (w, 1e-6), (None, 0.0)]
+    with torch.no_grad():
+        ms_k = timed(lambda: _qkv.qkv_project(hid, ws3, nrm, freqs))
+        ms_kt = timed(lambda: _qkv.qkv_project(hid, ws3, nrm, freqs, keep_for_backward=True))
+    res["project_qkv_forward"]["kernel_ms"] = round(ms_k, 4)
+    res["project_qkv_forward"]["kernel_tflops"] = round(gemm_flop / (ms_k * 1e-3) / 1e12, 1)
+    res["project_qkv_forward"]["kernel_frac_bf16_peak"] = round(gemm_flop / (ms_k * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)
+    res["project_qkv_forward"]["kernel_keep_for_backward_ms"] = round(ms_kt, 4)
 
     w_cat = torch.cat([m.weight for m in lin], 0)
     qkv = torch.empty((B, T, 3 * dim), device=dev, dtype=torch.bfloat16)

@@ -74,6 +74,24 @@ HARP_QK_F32 = 0
 HARP_QK_BF16 = 1
 _f = ctypes.c_float
 _i64 = ctypes.c_int64
+
+
+class QkvOut(ctypes.Structure):
+    """harp_qkv_out_t of include/harp_qk_norm_rope.h (one projection of harp_qkv_project)."""
+
+    _fields_ = [
+        ("weight", _p),
+        ("ld_weight", _i64),
+        ("y", _p),
+        ("ld_y", _i64),
+        ("y_lin", _p),
+        ("norm_weight", _p),
+        ("norm_weight_dtype", _i),
+        ("eps", _f),
+        ("rms", _p),
+    ]
+
+
 # (restype, argtypes) of every symbol include/harp_qk_norm_rope.h declares
 QK_PROTOTYPES = {
     "harp_qk_rmsnorm_forward": (_i, [_p, _i64p, _p, _i64p, _p, _i, _p, _f, _i, _i, _i, _i, _p]),
@@ -87,6 +105,7 @@ QK_PROTOTYPES = {
     "harp_qk_norm_rope_backward_noalloc": (_i, [_p, _i64p, _p, _i64p, _p, _i, _p, _p, _i64, _i64, _p, _i64p, _p,
                                                 _i, _i, _i, _i, _i, _p]),
     "harp_qk_backward_workspace_bytes": (_sz, [_i, _i, _i, _i]),
+    "harp_qkv_project": (_i, [_p, _i64, _i, _i, _i, _i, _p, _i64, _i64, ctypes.POINTER(QkvOut), _i, _p]),
     "harp_qk_last_error": (ctypes.c_char_p, []),
 }
 

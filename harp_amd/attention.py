@@ -6,12 +6,13 @@ attn.py:51-105): it wraps the model's pretrained attention module (``to_q``,
 ``ZAttention`` of src/models/z_image/standalone_transformer.py:197-225) and
 runs, for ``hidden_states`` [B, S, dim]:
 
-1. the three projections (plain library GEMMs: ``nn.Linear`` on the HIP
-   device, i.e. hipBLASLt), viewed as token-major [B, H, S, D] without a copy
-   (attn.py:69-76);
-2. QK RMSNorm and RoPE (attn.py:78-89) as one fused pass per tensor
-   (:class:`QKNormRopeFn`), or the separate operator when only one of the two
-   applies, writing the token-major layout the ring kernel reads;
+1. the three projections, viewed as token-major [B, H, S, D] (attn.py:69-76);
+2. QK RMSNorm and RoPE (attn.py:78-89), writing the token-major layout the
+   ring kernel reads.  Steps 1-2 are one launch of the fused projection
+   kernel (:mod:`harp_amd.qkv`) where it applies (head dim 128, no bias);
+   otherwise plain library GEMMs (``nn.Linear``, hipBLASLt) and one fused
+   norm + RoPE pass per tensor (:class:`QKNormRopeFn`), or the separate
+   operator when only one of the two applies;
 3. :class:`RingAttention` over ``sp_size`` KV chunks of the sequence (all on
    this GPU), then ``transpose(1, 2).flatten(2, 3)`` and ``to_out``
    (attn.py:99-103).
@@ -29,6 +30,7 @@ from torch import nn
 
 from .ops import RingAttention
 from .qk import ApplyRotaryComplexFn, QKNormRopeFn, RMSNormFn
+from .qkv import ProjectQKVFn, fused_supported
 
 
 def _norm_rope(x: torch.Tensor, norm: Optional[nn.Module], freqs_cis: Optional[torch.Tensor]) -> torch.Tensor:
@@ -45,10 +47,18 @@ def _norm_rope(x: torch.Tensor, norm: Optional[nn.Module], freqs_cis: Optional[t
     return x
 
 
-def project_qkv(attn: nn.Module, hidden_states: torch.Tensor,
-                freqs_cis: Optional[torch.Tensor]) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+def project_qkv(attn: nn.Module, hidden_states: torch.Tensor, freqs_cis: Optional[torch.Tensor],
+                fused: bool = True) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """q, k, v as token-major [B, H, S, D] views: projections, then QK RMSNorm
-    and RoPE (attn.py:69-89)."""
+    and RoPE (attn.py:69-89).  With ``fused`` (default) and a module and input
+    the fused kernel takes (:func:`harp_amd.qkv.fused_supported`: head dim
+    128, no bias), all of it is one launch (:class:`ProjectQKVFn`); otherwise
+    three library GEMMs and the separate norm + RoPE kernels."""
+    if fused and fused_supported(attn, hidden_states, freqs_cis):
+        nq, nk = getattr(attn, "norm_q", None), getattr(attn, "norm_k", None)
+        return ProjectQKVFn.apply(hidden_states, attn.to_q.weight, attn.to_k.weight, attn.to_v.weight,
+                                  None if nq is None else nq.weight, None if nk is None else nk.weight, freqs_cis,
+                                  0.0 if nq is None else float(nq.eps), 0.0 if nk is None else float(nk.eps))
     heads = attn.heads
     query = attn.to_q(hidden_states).unflatten(-1, (heads, -1)).transpose(1, 2)
     key = attn.to_k(hidden_states).unflatten(-1, (heads, -1)).transpose(1, 2)

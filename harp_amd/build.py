@@ -36,9 +36,9 @@ OPS_LIB = OUT / "libring_attention_ops.so"
 ASYNC_OPS_LIB = OUT / "libharp_async_op.so"
 PROBE_LIB = OUT / "libharp_probe.so"
 
-HIP_SOURCES = ["ra_kernels.hip", "ra_abi.hip", "qk_kernels.hip", "qk_abi.hip"]
+HIP_SOURCES = ["ra_kernels.hip", "ra_abi.hip", "qk_kernels.hip", "qk_abi.hip", "proj_kernels.hip"]
 PROBE_SOURCE = "bench/mfma_probe.hip"
-HIP_HEADERS = ["ra_common.h", "ra_kernels.h", "qk_kernels.h"]
+HIP_HEADERS = ["ra_common.h", "ra_kernels.h", "qk_kernels.h", "proj_kernels.h"]
 OPS_SOURCE = "torch_ring_attention_ops.cpp"
 ASYNC_OPS_SOURCE = "torch_async_op.cpp"
 

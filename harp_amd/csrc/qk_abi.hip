@@ -17,6 +17,7 @@
 #include <vector>
 
 #include "../../include/harp_qk_norm_rope.h"
+#include "proj_kernels.h"
 #include "qk_kernels.h"
 
 using namespace harp_qk;
@@ -326,6 +327,66 @@ int harp_qk_norm_rope_backward_noalloc(const void* dy, const int64_t* dy_strides
   if ((rc = scratch_ptr(&ws))) return rc;
   return backward(3, dy, dy_strides, x, x_strides, weight, weight_dtype, rms, freqs, f_stride_b, f_stride_s, dx,
                   dx_strides, grad_weight, grad_weight_dtype, batch, h_num, s_len, h_len, ws, sizeof(scratch), stream);
+}
+
+int harp_qkv_project(const void* x, int64_t ld_x, int batch, int seq, int k_dim, int n_out, const float* freqs,
+                     int64_t f_stride_b, int64_t f_stride_s, const harp_qkv_out_t* outs, int n_outs, void* stream) {
+  using harp_proj::kHeadDim;
+  using harp_proj::kKTile;
+  auto aligned16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; };
+  constexpr int64_t kMaxLd = (int64_t)1 << 22;  // a 256-row tile spans < 2^32 bytes
+  if (!x || !aligned16(x)) return fail(HARP_QK_EINVAL, "x must be a 16-byte aligned device pointer");
+  if (batch < 1 || seq < 1) return fail(HARP_QK_EINVAL, "batch=%d and seq=%d must be positive", batch, seq);
+  if ((int64_t)batch * seq >= ((int64_t)1 << 31)) return fail(HARP_QK_EUNSUPPORTED, "batch * seq >= 2^31");
+  if (k_dim < kKTile || k_dim % kKTile)
+    return fail(HARP_QK_EUNSUPPORTED, "k_dim=%d must be a positive multiple of %d", k_dim, kKTile);
+  if (n_out < kHeadDim || n_out % kHeadDim)
+    return fail(HARP_QK_EUNSUPPORTED, "n_out=%d must be a positive multiple of %d (heads of 128)", n_out, kHeadDim);
+  if (ld_x < k_dim || ld_x % 8 || ld_x > kMaxLd)
+    return fail(HARP_QK_EINVAL, "ld_x=%lld must be a multiple of 8 in [k_dim, 2^22]", (long long)ld_x);
+  if (!outs || n_outs < 1 || n_outs > harp_proj::kMaxOuts)
+    return fail(HARP_QK_EINVAL, "outs must hold 1 to %d outputs (got %d)", harp_proj::kMaxOuts, n_outs);
+  int rc;
+  if (freqs && (rc = check_freqs(freqs, f_stride_b, f_stride_s))) return rc;
+  harp_proj::ProjParams p{};
+  p.x = (const uint16_t*)x;
+  p.ldx = ld_x;
+  p.M = batch * seq;
+  p.S = seq;
+  p.K = k_dim;
+  p.heads = n_out / kHeadDim;
+  p.freqs = freqs;
+  p.f_stride_b = f_stride_b;
+  p.f_stride_s = f_stride_s;
+  p.n_outs = n_outs;
+  for (int i = 0; i < n_outs; ++i) {
+    const harp_qkv_out_t& o = outs[i];
+    if (!o.weight || !aligned16(o.weight)) return fail(HARP_QK_EINVAL, "outs[%d].weight must be 16-byte aligned", i);
+    if (o.ld_weight < k_dim || o.ld_weight % 8 || o.ld_weight > kMaxLd)
+      return fail(HARP_QK_EINVAL, "outs[%d].ld_weight=%lld must be a multiple of 8 in [k_dim, 2^22]", i,
+                  (long long)o.ld_weight);
+    if (!o.y || !aligned16(o.y)) return fail(HARP_QK_EINVAL, "outs[%d].y must be 16-byte aligned", i);
+    if (o.ld_y < n_out || o.ld_y % 8)
+      return fail(HARP_QK_EINVAL, "outs[%d].ld_y=%lld must be a multiple of 8 >= n_out", i, (long long)o.ld_y);
+    if (o.y_lin && !aligned16(o.y_lin)) return fail(HARP_QK_EINVAL, "outs[%d].y_lin must be 16-byte aligned", i);
+    if (o.norm_weight) {
+      if ((rc = check_weight(o.norm_weight, o.norm_weight_dtype))) return rc;
+    } else if (o.y_lin || o.rms) {
+      return fail(HARP_QK_EINVAL, "outs[%d]: y_lin and rms belong to outputs with a norm_weight", i);
+    }
+    harp_proj::ProjOut& q = p.out[i];
+    q.w = (const uint16_t*)o.weight;
+    q.ldw = o.ld_weight;
+    q.y = (uint16_t*)o.y;
+    q.ldy = o.ld_y;
+    q.y_lin = (uint16_t*)o.y_lin;
+    q.norm_w = o.norm_weight;
+    q.norm_w_f32 = o.norm_weight && o.norm_weight_dtype == HARP_QK_F32;
+    q.eps = o.eps;
+    q.rms = o.rms;
+  }
+  if ((rc = launched(harp_proj::launch_proj(p, (hipStream_t)stream), "qkv projection"))) return rc;
+  return ok();
 }
 
 }  // extern "C"

@@ -27,11 +27,6 @@
 
 namespace harp_ra {
 
-typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
-typedef __attribute__((address_space(3))) void lds_void;
-typedef uint32_t rsrc_t __attribute__((ext_vector_type(4)));  // buffer resource (V#), SGPR quad
-
-constexpr uint32_t kOOB = 0x80000000u;  // buffer offset past every valid range: loads 0
 
 // LDS is 64 banks x 4 bytes (256 bytes per cycle); 16-byte accesses are
 // served 16 lanes per cycle, 8-byte accesses 32 lanes per cycle.  Two tile
@@ -74,58 +69,6 @@ struct PadTile {
   }
 };
 
-// Raw buffer descriptor: base address, stride 0, num_records = bytes, and the
-// dword-3 format word of an untyped buffer.  The base and size are
-// wave-uniform by construction; readfirstlane tells the compiler so, which
-// keeps the descriptor in SGPRs.
-__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  const uint64_t a = (uint64_t)base;
-  rsrc_t r;
-  r.x = __builtin_amdgcn_readfirstlane((uint32_t)a);
-  r.y = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32)) & 0xffffu;
-  r.z = __builtin_amdgcn_readfirstlane(bytes);
-  r.w = 0x00020000u;
-  return r;
-}
-
-// Buffer resource over rows [row0, row0 + rows) of a [rows][stride] bf16 view.
-__device__ __forceinline__ rsrc_t rows_rsrc(const bf16* base, int64_t stride, int row0, int rows) {
-  return make_rsrc(base + (int64_t)row0 * stride, (uint32_t)((int64_t)(rows > 0 ? rows : 0) * stride * 2));
-}
-
-// One direct-to-LDS copy: every lane's 16 bytes at buffer offset voff land at
-// LDS byte address lds + 16 * lane (M0 holds the wave-uniform base; one wait
-// state separates the M0 write from its use).
-// Issued as inline asm on purpose: the compiler cannot tell which LDS buffer
-// an LDS-DMA load writes, so for the builtin it makes every later LDS read
-// wait for the load (s_waitcnt vmcnt(0)), which turns the double-buffered
-// prefetch into a synchronous load per tile.  Completion is instead ordered
-// explicitly: wait_lds_loads() then a barrier, before any wave reads the
-// buffer, and no load targets a buffer until a barrier shows that every wave
-// has finished reading it.
-__device__ __forceinline__ void lds_dma_b128(rsrc_t rs, uint32_t lds, uint32_t voff) {
-  asm volatile(
-      "s_mov_b32 m0, %0\n\t"
-      "s_nop 0\n\t"
-      "buffer_load_dwordx4 %1, %2, 0 offen lds"
-      :
-      : "s"(lds), "v"(voff), "s"(rs)
-      : "memory", "m0");
-}
-
-// The same with 4 bytes per lane: lane i's dword lands at lds + 4 * i.
-__device__ __forceinline__ void lds_dma_b32(rsrc_t rs, uint32_t lds, uint32_t voff) {
-  asm volatile(
-      "s_mov_b32 m0, %0\n\t"
-      "s_nop 0\n\t"
-      "buffer_load_dword %1, %2, 0 offen lds"
-      :
-      : "s"(lds), "v"(voff), "s"(rs)
-      : "memory", "m0");
-}
-
-// Wait for this thread's direct-to-LDS loads (a barrier then publishes them).
-__device__ __forceinline__ void wait_lds_loads() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // This wave's share of the direct-to-LDS copies of one 64-row tile: slot
 // instruction i (64 slots) goes to waves round-robin; voff holds each lane's
@@ -257,14 +200,6 @@ struct XorLanes {
   }
 };
 
-// Settle a value loaded from global memory before the main loop.  The
-// direct-to-LDS loads are invisible to the compiler, but they count in the
-// same hardware vmcnt: a wait the compiler places inside the loop for a
-// prologue load would also wait for the tile loads just issued.  An asm that
-// reads (and nominally rewrites) the value makes the compiler wait once,
-// here, and leaves nothing for it to wait on inside the loop.
-__device__ __forceinline__ void settle(bf16x8& x) { asm volatile("" : "+v"(x)); }
-__device__ __forceinline__ void settle(float& x) { asm volatile("" : "+v"(x)); }
 
 // Wave issue priority (s_setprio, 0..3) within a tile.  Two waves share a
 // SIMD and the issue arbiter otherwise favours the older one, which then
@@ -276,8 +211,6 @@ __device__ __forceinline__ void prio() {
   __builtin_amdgcn_s_setprio(LEVEL);
 }
 
-// Scheduling fence: the compiler may not move any instruction across it.
-__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
 
 // Compile-time step index: converts to int, and generic lambdas can read it
 // as a constant expression (decltype(i)::value).

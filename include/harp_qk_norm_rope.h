@@ -153,6 +153,48 @@ HARP_QK_API int harp_qk_norm_rope_backward_noalloc(const void* dy, const int64_t
  * (2048 + 32) x h_len floats. */
 HARP_QK_API size_t harp_qk_backward_workspace_bytes(int batch, int h_num, int s_len, int h_len);
 
+/*
+ * The producer of the ring-attention block's q, k and v in one launch: up to
+ * three projections y = x W^T (nn.Linear without bias) of the hidden states
+ * x [batch * seq, k_dim] (row stride ld_x, token b * seq + s), each written
+ * as y [batch * seq, n_out] (row stride ld_y): the token-major [B, S, H, 128]
+ * layout the ring-attention operators read as [B, H, S, 128] views.
+ * For an output with a norm_weight, every 128-feature head of the product,
+ * rounded to bf16 to nearest (as the Linear layer's output), is normalised
+ * as by harp_qk_norm_rope_forward (RMSNorm with eps and the [128] weight,
+ * then RoPE with row s of freqs when freqs is not NULL; fp32 arithmetic, bf16
+ * results truncated) before its only store; y_lin (may be NULL) receives the
+ * bf16 product itself and rms (may be NULL) the fp32 rms at
+ * (b * (n_out / 128) + h) * seq + s, the two tensors
+ * harp_qk_norm_rope_backward takes.  An output without norm_weight is the
+ * plain product (its y_lin and rms must be NULL).
+ * Requirements: n_out a positive multiple of 128 and k_dim of 64 (else
+ * HARP_QK_EUNSUPPORTED); k_dim <= ld_x, ld_weight <= 2^22 and n_out <= ld_y,
+ * all multiples of 8 elements; x, weights, y, y_lin, norm weights 16-byte
+ * aligned; batch * seq < 2^31.  freqs as for harp_qk_rope_forward with
+ * D = 128 (pair p of token (b, s) at freqs + b*f_stride_b + s*f_stride_s + 2p).
+ * Outputs must not overlap each other or the inputs.  Asynchronous on stream;
+ * no workspace, no allocation.
+ * Replaces: the three projections and the norm_q / norm_k and RoPE calls of
+ *   Z_Attention.forward, src/models/z_image/module/attn.py:69-89 (nn.Linear,
+ *   then async_rt/csrc/rms_norm.cc:20-105 and rope.cc:9-86 on the CPU).
+ */
+typedef struct harp_qkv_out {
+  const void* weight;      /* [n_out, k_dim] bf16, row stride ld_weight */
+  int64_t ld_weight;
+  void* y;                 /* [batch * seq, n_out] bf16, row stride ld_y */
+  int64_t ld_y;
+  void* y_lin;             /* NULL, or like y: the bf16 product before RMSNorm */
+  const void* norm_weight; /* NULL (plain projection) or [128] */
+  int norm_weight_dtype;   /* HARP_QK_BF16 or HARP_QK_F32 */
+  float eps;
+  float* rms;              /* NULL or [batch * (n_out / 128) * seq] fp32 */
+} harp_qkv_out_t;
+
+HARP_QK_API int harp_qkv_project(const void* x, int64_t ld_x, int batch, int seq, int k_dim, int n_out,
+                                 const float* freqs, int64_t f_stride_b, int64_t f_stride_s,
+                                 const harp_qkv_out_t* outs, int n_outs, void* stream);
+
 /* Last error message of the calling thread ("" if none). */
 HARP_QK_API const char* harp_qk_last_error(void);
 

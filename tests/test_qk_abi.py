@@ -29,12 +29,12 @@ REF_SCHEMAS = {
 
 def header_functions():
     text = open(HEADER).read()
-    return sorted(set(re.findall(r"HARP_QK_API\s+[\w\s\*]+?\b(harp_qk_\w+)\s*\(", text)))
+    return sorted(set(re.findall(r"HARP_QK_API\s+[\w\s\*]+?\b(harp_qkv?_\w+)\s*\(", text)))
 
 
 def test_header_and_prototypes_agree():
     fns = header_functions()
-    assert len(fns) == 9
+    assert len(fns) == 10
     assert set(fns) == set(_lib.QK_PROTOTYPES)
 
 
@@ -44,7 +44,7 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(lib, name), name
     nm = subprocess.run(["nm", "-D", "--defined-only", str(_lib.ABI_LIB)], capture_output=True, text=True)
     exported = {ln.split()[-1] for ln in nm.stdout.splitlines() if " T " in ln}
-    assert {s for s in exported if s.startswith("harp_qk_")} == set(header_functions())
+    assert {s for s in exported if s.startswith(("harp_qk_", "harp_qkv_"))} == set(header_functions())
 
 
 def _strides(b, h, s, d=1):
@@ -95,6 +95,50 @@ def test_backward_validation_and_workspace_size():
     # capped at 2048 blocks (+ 32 groups of 64)
     assert lib.harp_qk_backward_workspace_bytes(1, 24, 8192, 128) == (2048 + 32) * 128 * 4
     assert lib.harp_qk_backward_workspace_bytes(1, 8, 64, 100) == 2 ** 64 - 1
+
+
+def _qkv(over_outs=None, **over):
+    """harp_qkv_project with valid-looking arguments (fake, aligned pointers)
+    except for the given overrides; validation must fail before any launch."""
+    lib = harp_amd.load_abi()
+    outs = (_lib.QkvOut * 3)()
+    for o in outs:
+        o.weight, o.ld_weight, o.y, o.ld_y = FAKE, 256, FAKE, 256
+        o.y_lin, o.norm_weight, o.norm_weight_dtype, o.eps, o.rms = None, FAKE, _lib.HARP_QK_BF16, 1e-6, None
+    for i, kv in (over_outs or {}).items():
+        for k, v in kv.items():
+            setattr(outs[i], k, v)
+    a = dict(x=FAKE, ldx=256, B=1, S=64, K=256, n_out=256, f=FAKE, fsb=0, fss=128, n_outs=3)
+    a.update(over)
+    rc = lib.harp_qkv_project(a["x"], a["ldx"], a["B"], a["S"], a["K"], a["n_out"], a["f"], a["fsb"], a["fss"],
+                              outs, a["n_outs"], None)
+    return rc, lib.harp_qk_last_error().decode()
+
+
+@pytest.mark.parametrize(
+    "over,outs_over,code,msg",
+    [
+        (dict(K=100), None, 2, "k_dim"),
+        (dict(K=0), None, 2, "k_dim"),
+        (dict(n_out=200), None, 2, "n_out"),
+        (dict(x=FAKE + 2), None, 1, "x must"),
+        (dict(ldx=128), None, 1, "ld_x"),
+        (dict(ldx=260), None, 1, "ld_x"),
+        (dict(B=0), None, 1, "batch"),
+        (dict(n_outs=0), None, 1, "outs"),
+        (dict(n_outs=4), None, 1, "outs"),
+        (dict(fss=3), None, 1, "freqs"),
+        ({}, {1: dict(weight=None)}, 1, "outs[1].weight"),
+        ({}, {0: dict(ld_weight=100)}, 1, "ld_weight"),
+        ({}, {2: dict(ld_y=128)}, 1, "ld_y"),
+        ({}, {0: dict(y=FAKE + 8)}, 1, "outs[0].y"),
+        ({}, {2: dict(norm_weight=None, y_lin=FAKE)}, 1, "y_lin and rms"),
+        ({}, {1: dict(norm_weight_dtype=7)}, 1, "dtype"),
+    ],
+)
+def test_qkv_project_rejects_bad_arguments_on_the_host(over, outs_over, code, msg):
+    rc, err = _qkv(outs_over, **over)
+    assert rc == code and msg in err, (rc, err)
 
 
 def test_async_op_schemas_are_the_references():
