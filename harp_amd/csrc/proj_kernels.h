@@ -37,9 +37,12 @@ struct ProjParams {
   int64_t f_stride_b, f_stride_s;
   int n_outs;
   ProjOut out[kMaxOuts];
+  // set by launch_proj: blocks per output of the main grid, the first block of
+  // the last output left to the tail launch, and its first unit there
+  int n_lin, keep_last, tail_bid0;
 };
 
-// LDS bytes of the kernel: two stages of the x and W tiles
+// LDS bytes of the main kernel: two stages of the x and W tiles
 constexpr int kProjLdsBytes = 2 * (kBlockTokens + kBlockHeads * kHeadDim) * kKTile * 2;
 
 hipError_t launch_proj(const ProjParams& p, hipStream_t stream);

@@ -118,6 +118,33 @@ def test_fused_producer_matches_oracle(B, S, dim, heads, nwk, rope, batched):
         assert_pairs_close(bits(out), bits(sep), what=f"{name} vs separate kernel")
 
 
+@pytest.mark.parametrize("S,heads,n_outs", [(140 * 256 - 50, 2, 2), (90 * 256 - 200, 3, 3)])
+def test_tail_launch_matches_oracle(S, heads, n_outs):
+    """Shapes whose work units fill at most half of the CUs' last round: the
+    launcher runs those units as 128-token halves in a second launch.  The
+    tail then covers the last output's final units, including the partial
+    last token tile (and, with 3 heads, the half-empty last head pair)."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    units = n_outs * ((heads + 1) // 2) * math.ceil(S / 256)
+    r = units % cus
+    assert units > cus and 0 < r <= cus // 2, (units, cus)  # the case under test
+    print(f"[qkv tail S={S} heads={heads} outs={n_outs}: {r} units in the tail launch]", flush=True)
+    x, ws, norms, fc, f_np = _inputs(1, S, 128, heads, "bf16", True, False, seed=S)
+    norms = norms + [(None, 0.0)]
+    outs, lins, rmss = qkv.qkv_project(x, ws[:n_outs], norms[:n_outs], fc, keep_for_backward=True)
+    torch.cuda.synchronize()
+    for i in range(n_outs):
+        nw, eps = norms[i]
+        if nw is None:
+            _check_product(x, ws[i], outs[i], f"out {i}")
+            continue
+        _check_product(x, ws[i], lins[i], f"out {i} product")
+        lin4 = lins[i].unflatten(-1, (heads, 128)).transpose(1, 2)
+        want, want_rms = qo.norm_rope_forward(bits(lin4), bits(nw), eps, f_np)
+        assert_pairs_close(bits(outs[i]), want, what=f"out {i} vs oracle")
+        np.testing.assert_allclose(rmss[i].cpu().numpy().reshape(want_rms.shape), want_rms, rtol=1e-5)
+
+
 def _module(dim, heads, seed, bias=False):
     from types import SimpleNamespace
 
