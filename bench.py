@@ -239,8 +239,8 @@ def producer_bench(cfg, seed: int, iters: int = 20):
     hid = torch.randn((B, T, dim), generator=g).to(torch.bfloat16).to(dev)
     gemm_flop = 3 * 2 * B * T * dim * dim
 
-    def timed(fn, n=iters):
-        for _ in range(3):
+    def timed(fn, n=iters, warm=10):
+        for _ in range(warm):
             fn()
         e = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
         torch.cuda.synchronize()
@@ -254,8 +254,13 @@ def producer_bench(cfg, seed: int, iters: int = 20):
     # the producer as harp_amd.project_qkv runs it (fused kernel: projections
     # with norm + RoPE in the epilogue), and the unfused path beside it
     with torch.no_grad():
-        ms = timed(lambda: harp_amd.project_qkv(attn, hid, freqs))
-        ms_unfused = timed(lambda: harp_amd.project_qkv(attn, hid, freqs, fused=False))
+        # the two paths alternated twice after a warm-up of both (the board's
+        # clock settles over the first calls), mean of the two measurements each
+        timed(lambda: harp_amd.project_qkv(attn, hid, freqs), n=20)
+        runs = [(timed(lambda: harp_amd.project_qkv(attn, hid, freqs)),
+                 timed(lambda: harp_amd.project_qkv(attn, hid, freqs, fused=False))) for _ in range(2)]
+        ms = sum(r[0] for r in runs) / 2
+        ms_unfused = sum(r[1] for r in runs) / 2
     res["project_qkv_forward"] = {
         "avg_ms": round(ms, 4),
         "gemm_flop": gemm_flop,

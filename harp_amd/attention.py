@@ -30,7 +30,7 @@ from torch import nn
 
 from .ops import RingAttention
 from .qk import ApplyRotaryComplexFn, QKNormRopeFn, RMSNormFn
-from .qkv import ProjectQKVFn, fused_supported
+from .qkv import ProjectQKVFn, fused_supported, qkv_project
 
 
 def _norm_rope(x: torch.Tensor, norm: Optional[nn.Module], freqs_cis: Optional[torch.Tensor]) -> torch.Tensor:
@@ -56,9 +56,16 @@ def project_qkv(attn: nn.Module, hidden_states: torch.Tensor, freqs_cis: Optiona
     three library GEMMs and the separate norm + RoPE kernels."""
     if fused and fused_supported(attn, hidden_states, freqs_cis):
         nq, nk = getattr(attn, "norm_q", None), getattr(attn, "norm_k", None)
-        return ProjectQKVFn.apply(hidden_states, attn.to_q.weight, attn.to_k.weight, attn.to_v.weight,
-                                  None if nq is None else nq.weight, None if nk is None else nk.weight, freqs_cis,
-                                  0.0 if nq is None else float(nq.eps), 0.0 if nk is None else float(nk.eps))
+        args = (hidden_states, attn.to_q.weight, attn.to_k.weight, attn.to_v.weight,
+                None if nq is None else nq.weight, None if nk is None else nk.weight, freqs_cis,
+                0.0 if nq is None else float(nq.eps), 0.0 if nk is None else float(nk.eps))
+        if torch.is_grad_enabled() and any(isinstance(a, torch.Tensor) and a.requires_grad for a in args):
+            return ProjectQKVFn.apply(*args)
+        # no gradient can be taken: the kernel alone, without the pre-norm
+        # products and rms a backward would need
+        (q, k, v), _, _ = qkv_project(args[0], args[1:4], [(args[4], args[7]), (args[5], args[8]), (None, 0.0)],
+                                      freqs_cis)
+        return q, k, v
     heads = attn.heads
     query = attn.to_q(hidden_states).unflatten(-1, (heads, -1)).transpose(1, 2)
     key = attn.to_k(hidden_states).unflatten(-1, (heads, -1)).transpose(1, 2)

@@ -144,7 +144,9 @@ class ProjectQKVFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, hidden, wq, wk, wv, nwq, nwk, freqs_cis, eps_q, eps_k):
         norms = [(nwq, eps_q), (nwk, eps_k), (None, 0.0)]
-        # the pre-norm products and rms are written only when a gradient will be asked for
+        # the pre-norm products and rms are written only when a gradient can be
+        # asked for (needs_input_grad follows requires_grad, also under no_grad:
+        # callers that take no gradient call qkv_project directly)
         keep = any(ctx.needs_input_grad)
         (q, k, v), lins, rmss = qkv_project(hidden, [wq, wk, wv], norms, freqs_cis, keep_for_backward=keep)
         ctx.save_for_backward(hidden, wq, wk, wv, nwq, nwk, freqs_cis, lins[0], lins[1], rmss[0], rmss[1])

@@ -173,9 +173,13 @@ def test_project_qkv_takes_the_fused_path_only_where_it_applies():
     with torch.no_grad():
         fused = project_qkv(attn, x, fc)
         unfused = project_qkv(attn, x, fc, fused=False)
+    assert all(t.grad_fn is None for t in fused)  # no gradient possible: the kernel alone
     for a, b, name in zip(fused, unfused, "qkv"):
         rel = ((a.double() - b.double()).norm() / b.double().norm()).item()
         assert rel <= 4e-3, (name, rel)
+    q, k, v = project_qkv(attn, x, fc)  # weights require grad: the autograd Function
+    assert all(t.grad_fn is not None for t in (q, k, v))
+    assert torch.equal(q, fused[0]) and torch.equal(k, fused[1]) and torch.equal(v, fused[2])
 
 
 @pytest.mark.parametrize("B,S,dim,heads,rope", [(2, 256, 256, 2, True), (1, 300, 192, 3, False)])
