@@ -96,9 +96,23 @@ def qkv_project(hidden_states: torch.Tensor, weights: Sequence[torch.Tensor],
     keep_for_backward the normalised outputs' bf16 products ([B, S, H*128])
     and rms ([B*H*S] fp32) are written too (else None)."""
     x = hidden_states
+    if not (x.is_cuda and x.dtype == torch.bfloat16 and x.dim() == 3):
+        raise ValueError("hidden_states must be a [B, S, dim] bf16 tensor on a HIP device (there is no CPU path)")
     B, S, K = x.shape
-    x2 = x if x.is_contiguous() else x.contiguous()
+    if not 1 <= len(weights) <= 3:
+        raise ValueError(f"one to three weights, got {len(weights)}")
     n_out = weights[0].size(0)
+    if n_out % HEAD_DIM or K % K_TILE or K == 0:
+        raise ValueError(f"weights must be [heads*128, dim] with dim a multiple of {K_TILE}, got {tuple(weights[0].shape)}")
+    for w in weights:
+        if (w.dtype != torch.bfloat16 or w.device != x.device or tuple(w.shape) != (n_out, K) or w.stride(-1) != 1):
+            raise ValueError(f"every weight must be a bf16 [{n_out}, {K}] tensor with unit column stride on "
+                             f"{x.device}, got {w.dtype} {tuple(w.shape)} on {w.device}")
+    for nw, _ in norms:
+        if nw is not None and (nw.dtype not in (torch.bfloat16, torch.float32) or nw.device != x.device
+                               or nw.numel() != HEAD_DIM or not nw.is_contiguous()):
+            raise ValueError(f"RMSNorm weights must be contiguous [128] bf16 or fp32 tensors on {x.device}")
+    x2 = x if x.is_contiguous() else x.contiguous()
     H = n_out // HEAD_DIM
     M = B * S
     f = None

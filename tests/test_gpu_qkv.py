@@ -204,3 +204,19 @@ def test_fused_backward_matches_unfused_autograd(B, S, dim, heads, rope):
         rel = ((a.double() - b.double()).norm() / b.double().norm()).item()
         print(f"grad {name}: rel {rel:.2e}", flush=True)
         assert rel <= 1e-2, (name, rel)
+
+
+def test_qkv_project_refuses_mismatched_weights():
+    """Shapes the kernel cannot check (a weight's row count, the norm
+    weight's length) are refused on the host before any launch."""
+    x = torch.zeros((1, 64, 128), dtype=torch.bfloat16, device=DEV)
+    w = torch.zeros((256, 128), dtype=torch.bfloat16, device=DEV)
+    nw = torch.ones(128, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError, match="every weight"):
+        qkv.qkv_project(x, [w, w, w[:128]], [(nw, 1e-6), (nw, 1e-6), (None, 0.0)], None)
+    with pytest.raises(ValueError, match="every weight"):
+        qkv.qkv_project(x, [w, w.float(), w], [(nw, 1e-6), (nw, 1e-6), (None, 0.0)], None)
+    with pytest.raises(ValueError, match="RMSNorm weights"):
+        qkv.qkv_project(x, [w, w, w], [(nw[:64], 1e-6), (nw, 1e-6), (None, 0.0)], None)
+    with pytest.raises(ValueError, match="multiple of 64"):
+        qkv.qkv_project(x[..., :96].contiguous(), [w[:, :96].contiguous()] * 3, [(None, 0.0)] * 3, None)

@@ -189,3 +189,14 @@ def test_attention_block_on_cpu_tensors_raises():
         block(x, freqs)
     with pytest.raises(ValueError, match="multiple of sp_size"):
         harp_amd.RingZAttention(attn, 3)(x, freqs)
+
+
+def test_qkv_project_validates_shapes_before_the_kernel():
+    """harp_amd.qkv.qkv_project refuses CPU tensors and mismatched weights on
+    the host: the kernel itself cannot see a weight's row count."""
+    from harp_amd import qkv
+
+    x = torch.zeros((1, 8, 128), dtype=torch.bfloat16)
+    w = torch.zeros((256, 128), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="HIP device"):
+        qkv.qkv_project(x, [w, w, w], [(None, 0.0)] * 3, None)
