@@ -1,6 +1,7 @@
 """HIP-graph capture of the block's operators: ring-attention forward, delta
-and backward (torch.ops.ring_attention_ops) and the fused QK RMSNorm + RoPE
-forward and backward (torch.ops.async_op) are recorded once into a
+and backward (torch.ops.ring_attention_ops), the fused QK RMSNorm + RoPE
+forward and backward (torch.ops.async_op) and the fused q/k/v projection
+kernel (harp_amd.qkv) are recorded once into a
 torch.cuda.CUDAGraph on static tensors and replayed on new inputs.  No
 operator allocates device memory outside torch's allocator or clears memory
 with hipMemsetAsync, so each replay must equal the eager result on the same
@@ -120,4 +121,46 @@ def test_qk_norm_rope_graph_replays_equal_eager():
         step(nx, ndy, *ref)
         torch.cuda.synchronize()
         for name, a, b in zip(("y", "rms", "dx", "grad_weight"), got, ref):
+            assert torch.equal(a, b), name
+
+
+def test_fused_producer_graph_replays_equal_eager():
+    """The fused q/k/v projection kernel (harp_amd.qkv.qkv_project, with the
+    pre-norm products and rms kept) at a shape whose half-empty last round
+    goes to the tail launch: two launches in the graph."""
+    from harp_amd import qkv
+
+    B, S, dim, H = 1, 90 * 256, 128, 2
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn((B, S, dim), generator=g).to(torch.bfloat16).to(DEV)
+    ws = [(torch.randn((H * 128, dim), generator=g) / dim ** 0.5).to(torch.bfloat16).to(DEV) for _ in range(3)]
+    w = (1 + 0.1 * torch.randn(128, generator=g)).to(torch.bfloat16).to(DEV)
+    ang = torch.arange(S, dtype=torch.float64)[:, None] * (10000.0 ** (-2.0 * torch.arange(64) / 128))[None, :]
+    f = torch.polar(torch.ones_like(ang), ang).to(torch.complex64).to(DEV)
+    norms = [(w, 1e-6), (w, 1e-6), (None, 0.0)]
+
+    def step(x_):
+        outs, lins, rmss = qkv.qkv_project(x_, ws, norms, f, keep_for_backward=True)
+        return list(outs) + [lins[0], lins[1], rmss[0], rmss[1]]
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step(x)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static = step(x)
+
+    for _ in range(3):
+        nx = torch.randn((B, S, dim), generator=g).to(torch.bfloat16).to(DEV)
+        x.copy_(nx)
+        graph.replay()
+        torch.cuda.synchronize()
+        got = [t.clone() for t in static]
+        ref = step(nx)
+        torch.cuda.synchronize()
+        for name, a, b in zip(("q", "k", "v", "q_lin", "k_lin", "rms_q", "rms_k"), got, ref):
             assert torch.equal(a, b), name
