@@ -121,8 +121,9 @@ def cpu_baseline(cfg, target_s: float):
     on a bounded sample of the workload: query rows of one head (then whole
     heads, one at a time) against the full KV length, sized from a short probe
     so that one repetition takes about target_s / 4.  One warm-up and three
-    timed repetitions of that sample; the median is reported (BASELINE.md
-    section 5).  Returns the cpu_baseline JSON object."""
+    timed repetitions of that sample; the median is reported, with the three
+    times and the host's model, cores and bf16 / matrix flags.  Returns the
+    cpu_baseline JSON object."""
     import statistics
 
     import torch

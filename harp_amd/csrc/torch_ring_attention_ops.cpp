@@ -113,7 +113,7 @@ Chunks split_chunks(const char* op, const at::Tensor& q, const at::Tensor& k, co
                 ") with sp_size=", sp_size,
                 " > 1: the other ranks' chunks would come from peers, which one GPU does not have. Pass all ",
                 "sp_size chunks concatenated along dim 2 (k.size(2) == sp_size * q.size(2)), or give kv_chunk_len ",
-                "(INTEGRATION.md section 2)");
+                "(k.size(2) == sp_size * kv_chunk_len)");
   } else {
     TORCH_CHECK(false, "ring_attention_ops.", op, ": k.size(2)=", rows, " does not match sp_size=", sp_size,
                 " chunks of q.size(2)=", q.size(2), " rows; pass kv_chunk_len (k.size(2) == sp_size * kv_chunk_len) ",
