@@ -432,6 +432,10 @@ def main() -> int:
     # LDS (1 KB per MFMA per wave, 8 waves per CU); the LDS reads draw power
     # from the MFMA stream, so this is the ceiling for this kernel design
     lds_tf, lds_ghz = _lib.probe_mfma_lds_rate(False, 32768, args.seed)
+    # and at each kernel's own instruction mix: the same LDS-fed stream plus
+    # the kernel's measured VALU / exp / copy work per MFMA, with nothing
+    # waiting on anything -- the rate that mix allows on this board
+    mix = {k: _lib.probe_kernel_mix(k, 24576, args.seed) for k in kernel_mfma}
     kernels = {}
     for name, (ms, n) in kt.items():
         if n:
@@ -443,6 +447,10 @@ def main() -> int:
                 entry["tflops_mfma_performed"] = round(performed, 1)
                 entry["frac_of_sustained"] = round(performed / probe_tf, 4) if probe_tf > 0 else None
                 entry["frac_of_lds_fed"] = round(performed / lds_tf, 4) if lds_tf > 0 else None
+                mix_tf, mix_ghz = mix[name]
+                entry["mix_ceiling_tflops"] = round(mix_tf, 1)
+                entry["mix_ceiling_shader_ghz"] = round(mix_ghz, 3)
+                entry["frac_of_mix_ceiling"] = round(performed / mix_tf, 4) if mix_tf > 0 else None
             kernels[name] = entry
     dom = max((n for n in kernel_flops if n in kernels), key=lambda n: kt[n][0])
     dom_tf = kernels[dom]["tflops_algorithmic"]
@@ -487,6 +495,8 @@ def main() -> int:
             "lds_fed_mfma_tflops": round(lds_tf, 1),
             "lds_fed_mfma_shader_ghz": round(lds_ghz, 3),
             "frac_of_lds_fed": round(dom_tf / lds_tf, 4) if lds_tf > 0 else None,
+            "mix_ceiling_tflops": kernels[dom]["mix_ceiling_tflops"],
+            "frac_of_mix_ceiling": kernels[dom]["frac_of_mix_ceiling"],
         },
         "cpu_baseline": None,
         "gpu": torch.cuda.get_device_name(0),

@@ -197,6 +197,9 @@ def load_probe() -> ctypes.CDLL:
             lib.harp_probe_mfma_lds_rate.restype = _i
             lib.harp_probe_mfma_lds_rate.argtypes = [_i, ctypes.c_uint32, _i, ctypes.POINTER(ctypes.c_double),
                                                      ctypes.POINTER(ctypes.c_double)]
+            lib.harp_probe_kernel_mix.restype = _i
+            lib.harp_probe_kernel_mix.argtypes = [_i, _i, ctypes.c_uint32, ctypes.POINTER(ctypes.c_double),
+                                                  ctypes.POINTER(ctypes.c_double)]
             lib.harp_probe_last_error.restype = ctypes.c_char_p
             lib.harp_probe_last_error.argtypes = []
             _probe = lib
@@ -227,6 +230,25 @@ def probe_mfma_lds_rate(softmax: bool, iters: int = 8192, seed: int = 3407) -> t
                                       ctypes.byref(ghz))
     if rc != 0:
         raise RuntimeError(f"harp_probe_mfma_lds_rate failed (status {rc}): {lib.harp_probe_last_error().decode()}")
+    return tf.value, ghz.value
+
+
+PROBE_KERNELS = {"fwd": 0, "dkdv": 1, "dq": 2}
+
+
+def probe_kernel_mix(kernel: str, iters: int = 24576, seed: int = 3407) -> tuple:
+    """(TFLOP/s, shader GHz) of the LDS-fed MFMA stream carrying one attention
+    kernel's measured per-MFMA work besides (VALU instructions, exps and
+    direct-to-LDS copy bytes; kernel "fwd", "dkdv" or "dq"), with no
+    dependency between the streams: the rate that instruction mix allows on
+    this board under its power limit."""
+    lib = load_probe()
+    tf = ctypes.c_double()
+    ghz = ctypes.c_double()
+    rc = lib.harp_probe_kernel_mix(PROBE_KERNELS[kernel], int(iters), int(seed) & 0xFFFFFFFF, ctypes.byref(tf),
+                                   ctypes.byref(ghz))
+    if rc != 0:
+        raise RuntimeError(f"harp_probe_kernel_mix failed (status {rc}): {lib.harp_probe_last_error().decode()}")
     return tf.value, ghz.value
 
 

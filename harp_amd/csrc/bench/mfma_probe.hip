@@ -15,6 +15,18 @@
 //    other operand stays in registers, as Q, dO or P do in the kernels.
 // 3. harp_probe_mfma_lds_rate(softmax = 1): the same plus one v_exp_f32 and
 //    three FMAs per MFMA, the forward kernel's per-MFMA softmax work.
+// 4. harp_probe_kernel_mix(kernel): mix 2 at one attention kernel's measured
+//    per-MFMA work (hardware counters of the kernel at the headline shape):
+//    VALU instructions, of which v_exp_f32, and the bytes of direct-to-LDS
+//    copies it streams from L2 (buffer_load_dwordx4 ... lds, 1 KB per wave
+//    instruction, from a 1 MiB L2-resident buffer into a separate LDS area):
+//      kernel 0, forward: 4.5 VALU (1 exp), 128 B of copies per MFMA
+//      kernel 1, dK/dV:   2.5 VALU (0.5 exp), 64 B (its LDS reads are
+//                         1.1 KB per MFMA, the probe's 1 KB)
+//      kernel 2, dQ:      3.33 VALU (0.67 exp), 85 B
+//    Nothing in it depends on anything but its own registers: it is the rate
+//    that kernel's instruction mix allows on this board under its power
+//    limit, with no latency exposed and no wave waiting for another.
 // The board is power-limited under MFMA load: LDS reads and VALU work take
 // power from the MFMA stream, so mixes 2 and 3 run at a lower clock than 1.
 // They bound what a kernel with that operand path can reach, independently
@@ -27,6 +39,7 @@
 // C ABI (ctypes in harp_amd/_lib.py):
 //   int harp_probe_mfma_rate(int iters, uint32_t seed, double* tflops, double* shader_ghz);
 //   int harp_probe_mfma_lds_rate(int iters, uint32_t seed, int softmax, double* tflops, double* shader_ghz);
+//   int harp_probe_kernel_mix(int kernel, int iters, uint32_t seed, double* tflops, double* shader_ghz);
 //   const char* harp_probe_last_error(void);
 // Status 0 = ok, 1 = bad argument, 3 = allocation failed, 4 = launch failed.
 // Synchronous on the null stream; allocates and frees its own small buffers.
@@ -104,20 +117,38 @@ __global__ __launch_bounds__(256) void mfma_probe_kernel(uint32_t seed, int iter
   }
 }
 
-// Mixes 2 and 3: 8 waves, 64 KB of random bf16 in LDS.  The LDS reads and the
-// MFMAs that consume the previous step's fragments are one asm block, so the
-// compiler cannot sink the reads down to their use (which would expose their
-// latency) and the reads of step i + 1 overlap the MFMAs of step i.  Every
-// address is lane * 16 + group * 4096 + k * 1024 + 16 bytes <= 65536.
+// Mixes 2 to 4: 8 waves, 64 KB of random bf16 in LDS (plus 16 KB as the
+// copies' destination).  The LDS reads and the MFMAs that consume the
+// previous step's fragments are one asm block, so the compiler cannot sink
+// the reads down to their use (which would expose their latency) and the
+// reads of step i + 1 overlap the MFMAs of step i.  Every fragment address is
+// lane * 16 + group * 4096 + k * 1024 + 16 bytes <= 65536.
 constexpr int kLdsProbeWaves = 8;
 constexpr int kLdsProbeFrags = 64 * 64;  // bf16x8 fragments, 64 KB
+constexpr int kCopyLdsBytes = 2048 * kLdsProbeWaves;  // two 1 KB slots per wave
+constexpr uint32_t kCopySrcBytes = 1u << 20;         // L2-resident copy source
 
-template <bool SOFTMAX>
+// VALU work of one step (4 MFMAs): E exps and F FMAs on eight independent
+// chains whose values stay in (-3, 1).  The step's address arithmetic and
+// each copy's offset update add about 0.25 and 2 / COPY_EVERY / 4 VALU
+// instructions per MFMA; the mixes below count them.
+template <int E, int F>
+__device__ __forceinline__ void valu_work(float (&e)[8]) {
+#pragma unroll
+  for (int k = 0; k < E; ++k) e[k % 8] = __builtin_amdgcn_exp2f(e[k % 8]);
+#pragma unroll
+  for (int k = 0; k < F; ++k) e[(k + E) % 8] = __builtin_fmaf(e[(k + E) % 8], 0.5f, -1.5f);
+}
+
+// Steps cycle through three (exp, FMA) counts; a copy is issued every
+// COPY_EVERY steps (0: none).
+template <int E0, int F0, int E1, int F1, int E2, int F2, int COPY_EVERY>
 __global__ __launch_bounds__(64 * kLdsProbeWaves) void mfma_lds_probe_kernel(uint32_t seed, int iters, float* sink,
-                                                                            long long* clocks) {
-  __shared__ __attribute__((aligned(16))) bf16x8 lds[kLdsProbeFrags];
+                                                                            long long* clocks, const void* copy_src) {
+  __shared__ __attribute__((aligned(16))) bf16x8 lds[kLdsProbeFrags + kCopyLdsBytes / 16];
   const uint32_t gid = blockIdx.x * (64u * kLdsProbeWaves) + threadIdx.x;
   const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
   for (int i = threadIdx.x; i < kLdsProbeFrags; i += 64 * kLdsProbeWaves)
     lds[i] = random_bf16x8(hash32(seed + 7u) ^ (blockIdx.x * (uint32_t)kLdsProbeFrags + (uint32_t)i));
   __syncthreads();
@@ -128,8 +159,35 @@ __global__ __launch_bounds__(64 * kLdsProbeWaves) void mfma_lds_probe_kernel(uin
     x[0][j] = lds[j * 64 + lane];
     x[1][j] = x[0][j];
   }
-  float e[4] = {-0.01f * (float)lane, -0.5f, -0.25f, -1.f};
+  float e[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) e[k] = -0.01f * (float)(lane + k);
   const uint32_t base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)&lds[lane];
+  // copies: source offsets walk the 1 MiB buffer (wave-dependent start),
+  // destination alternates between the wave's two 1 KB slots
+  const uint64_t src = (uint64_t)(uintptr_t)copy_src;
+  uint32_t rsrc[4] = {(uint32_t)src, (uint32_t)(src >> 32) & 0xffffu, COPY_EVERY ? kCopySrcBytes : 0u, 0x00020000u};
+  const uint32_t copy_lds =
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)&lds[kLdsProbeFrags] + (uint32_t)wave * 2048u;
+  uint32_t voff = ((uint32_t)(blockIdx.x * kLdsProbeWaves + wave) * 8192u + (uint32_t)lane * 16u) & (kCopySrcBytes - 1u);
+  int n_copy = 0;
+  auto copy = [&]() {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 rs = {(uint32_t)__builtin_amdgcn_readfirstlane(rsrc[0]),
+                      (uint32_t)__builtin_amdgcn_readfirstlane(rsrc[1]),
+                      (uint32_t)__builtin_amdgcn_readfirstlane(rsrc[2]), rsrc[3]};
+    // at most four copies of this wave in flight
+    asm volatile(
+        "s_waitcnt vmcnt(3)\n\t"
+        "s_mov_b32 m0, %0\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %1, %2, 0 offen lds"
+        :
+        : "s"(copy_lds + (uint32_t)(n_copy & 1) * 1024u), "v"(voff), "s"(rs)
+        : "memory", "m0");
+    voff = (voff + 1024u) & (kCopySrcBytes - 1u);
+    ++n_copy;
+  };
   f32x16 c0 = zero16(), c1 = zero16(), c2 = zero16(), c3 = zero16();
   auto step = [&](const bf16x8* u, bf16x8* w, uint32_t addr) {
     asm volatile(
@@ -144,23 +202,29 @@ __global__ __launch_bounds__(64 * kLdsProbeWaves) void mfma_lds_probe_kernel(uin
         "s_waitcnt lgkmcnt(0)"
         : "+v"(c0), "+v"(c1), "+v"(c2), "+v"(c3), "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3])
         : "v"(u[0]), "v"(u[1]), "v"(u[2]), "v"(u[3]), "v"(b[0]), "v"(b[1]), "v"(b[2]), "v"(b[3]), "v"(addr));
-    if (SOFTMAX) {
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const float t = __builtin_amdgcn_exp2f(e[k]);
-        e[k] = __builtin_fmaf(t, -0.001f, e[k]);
-        e[k] = __builtin_fmaf(e[k], 0.999f, -0.0001f);
-        e[k] = __builtin_fmaf(e[k], 1.0001f, 0.00001f);
-      }
-    }
   };
+  auto addr_of = [&](int i) { return base + (uint32_t)((i & 15) * 4096); };
   const long long t0 = clock64(), r0 = wall_clock64();
-  for (int i = 0; i < iters; i += 2) {
-    step(x[0], x[1], base + (uint32_t)(((i + 1) & 15) * 4096));
-    step(x[1], x[0], base + (uint32_t)(((i + 2) & 15) * 4096));
+  // six steps per iteration: the fragment double buffer (2) times the
+  // three-step VALU cycle
+  for (int i = 0; i < iters; i += 6) {
+#define HARP_PROBE_STEP(k, E, F)                                   \
+  step(x[(k) & 1], x[((k) + 1) & 1], addr_of(i + (k) + 1));        \
+  valu_work<E, F>(e);                                              \
+  if (COPY_EVERY && ((i + (k)) % (COPY_EVERY ? COPY_EVERY : 1)) == 0) copy();
+    HARP_PROBE_STEP(0, E0, F0)
+    HARP_PROBE_STEP(1, E1, F1)
+    HARP_PROBE_STEP(2, E2, F2)
+    HARP_PROBE_STEP(3, E0, F0)
+    HARP_PROBE_STEP(4, E1, F1)
+    HARP_PROBE_STEP(5, E2, F2)
+#undef HARP_PROBE_STEP
   }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no copy may outlive the workgroup
   const long long t1 = clock64(), r1 = wall_clock64();
-  float s = e[0] + e[1] + e[2] + e[3];
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) s += e[k];
 #pragma unroll
   for (int j = 0; j < 16; ++j) s += c0[j] + c1[j] + c2[j] + c3[j];
   sink[gid] = s;
@@ -193,10 +257,39 @@ int launched(const char* what) {
 }
 
 // mix 0: register-fed, 32 waves per CU; mix 1 / 2: LDS-fed (without / with
-// the softmax VALU), 8 waves per CU
+// the softmax VALU), 8 waves per CU; mix 3 / 4 / 5: the forward / dK/dV / dQ
+// kernel's per-MFMA work, 8 waves per CU
+int launch_mix(int mix, int blocks, int threads, uint32_t sd, int iters, float* sink, long long* clocks,
+               const void* src) {
+  const dim3 g((unsigned)blocks), t((unsigned)threads);
+  switch (mix) {
+    case 0: hipLaunchKernelGGL(mfma_probe_kernel, g, t, 0, nullptr, sd, iters, sink, clocks); break;
+    case 1:
+      hipLaunchKernelGGL((mfma_lds_probe_kernel<0, 0, 0, 0, 0, 0, 0>), g, t, 0, nullptr, sd, iters, sink, clocks, src);
+      break;
+    case 2:
+      hipLaunchKernelGGL((mfma_lds_probe_kernel<4, 12, 4, 12, 4, 12, 0>), g, t, 0, nullptr, sd, iters, sink, clocks,
+                         src);
+      break;
+    case 3:  // forward: 4.5 VALU (1 exp) per MFMA, a 1 KB copy per 8 MFMAs
+      hipLaunchKernelGGL((mfma_lds_probe_kernel<4, 12, 4, 12, 4, 12, 2>), g, t, 0, nullptr, sd, iters, sink, clocks,
+                         src);
+      break;
+    case 4:  // dK/dV: 2.5 VALU (0.5 exp), a copy per 16 MFMAs
+      hipLaunchKernelGGL((mfma_lds_probe_kernel<2, 6, 2, 6, 2, 7, 4>), g, t, 0, nullptr, sd, iters, sink, clocks, src);
+      break;
+    default:  // dQ: 3.33 VALU (0.67 exp), a copy per 12 MFMAs
+      hipLaunchKernelGGL((mfma_lds_probe_kernel<3, 9, 3, 9, 2, 9, 3>), g, t, 0, nullptr, sd, iters, sink, clocks,
+                         src);
+      break;
+  }
+  return launched("MFMA probe");
+}
+
 int run_probe(int mix, int iters, uint32_t seed, double* tflops, double* shader_ghz) {
   if (!tflops || !shader_ghz) return fail(kEinval, "probe outputs are NULL");
   if (iters < 16 || iters > (1 << 20) || iters % 2) return fail(kEinval, "iters=%d must be even, in [16, 2^20]", iters);
+  if (mix > 0) iters = (iters + 5) / 6 * 6;  // the LDS-fed loops run six steps per iteration
   int dev = 0, cus = 0, wall_khz = 0;
   if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) ||
       hipDeviceGetAttribute(&wall_khz, hipDeviceAttributeWallClockRate, dev) || cus < 1 || wall_khz < 1)
@@ -206,30 +299,27 @@ int run_probe(int mix, int iters, uint32_t seed, double* tflops, double* shader_
   const int blocks = mix == 0 ? 8 * cus : cus;  // 32 or 8 waves per CU
   float* sink = nullptr;
   long long* clocks = nullptr;
+  void* src = nullptr;
   hipEvent_t e0 = nullptr, e1 = nullptr;
   int rc = kOk;
   std::vector<long long> h(2 * (size_t)blocks);
   float best_ms = 0.f;
   if (hipMalloc(&sink, sizeof(float) * threads * (size_t)blocks) != hipSuccess ||
-      hipMalloc(&clocks, sizeof(long long) * 2 * (size_t)blocks) != hipSuccess) {
+      hipMalloc(&clocks, sizeof(long long) * 2 * (size_t)blocks) != hipSuccess ||
+      hipMalloc(&src, kCopySrcBytes) != hipSuccess) {
     rc = fail(kEnomem, "probe buffers: hipMalloc failed");
   } else if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
     rc = fail(kElaunch, "probe events: hipEventCreate failed");
   } else {
+    // the copies' source: random bytes, so their data path toggles like real data
+    std::vector<uint32_t> r(kCopySrcBytes / 4);
+    for (size_t i = 0; i < r.size(); ++i) r[i] = (uint32_t)(i * 2654435761u) ^ (seed * 0x9e3779b9u) ^ (uint32_t)(i >> 7);
+    if (hipMemcpy(src, r.data(), kCopySrcBytes, hipMemcpyHostToDevice) != hipSuccess)
+      rc = fail(kElaunch, "probe copy source upload failed");
     // one warm-up launch (clocks ramp), then the timed one
     for (int rep = 0; rep < 2 && rc == kOk; ++rep) {
       (void)hipEventRecord(e0, nullptr);
-      const uint32_t sd = seed + (uint32_t)rep;
-      if (mix == 0)
-        hipLaunchKernelGGL(mfma_probe_kernel, dim3((unsigned)blocks), dim3(threads), 0, nullptr, sd, iters, sink,
-                           clocks);
-      else if (mix == 1)
-        hipLaunchKernelGGL(mfma_lds_probe_kernel<false>, dim3((unsigned)blocks), dim3(threads), 0, nullptr, sd, iters,
-                           sink, clocks);
-      else
-        hipLaunchKernelGGL(mfma_lds_probe_kernel<true>, dim3((unsigned)blocks), dim3(threads), 0, nullptr, sd, iters,
-                           sink, clocks);
-      if ((rc = launched("MFMA probe"))) break;
+      if ((rc = launch_mix(mix, blocks, threads, seed + (uint32_t)rep, iters, sink, clocks, src))) break;
       (void)hipEventRecord(e1, nullptr);
       if (hipEventSynchronize(e1) != hipSuccess || hipEventElapsedTime(&best_ms, e0, e1) != hipSuccess)
         rc = fail(kElaunch, "probe timing failed");
@@ -252,6 +342,7 @@ int run_probe(int mix, int iters, uint32_t seed, double* tflops, double* shader_
   if (e1) (void)hipEventDestroy(e1);
   if (sink) (void)hipFree(sink);
   if (clocks) (void)hipFree(clocks);
+  if (src) (void)hipFree(src);
   return rc == kOk ? ok() : rc;
 }
 
@@ -270,6 +361,12 @@ __attribute__((visibility("default"))) int harp_probe_mfma_lds_rate(int iters, u
                                                                     double* tflops, double* shader_ghz) {
   if (softmax != 0 && softmax != 1) return fail(kEinval, "softmax=%d must be 0 or 1", softmax);
   return run_probe(1 + softmax, iters, seed, tflops, shader_ghz);
+}
+
+__attribute__((visibility("default"))) int harp_probe_kernel_mix(int kernel, int iters, uint32_t seed, double* tflops,
+                                                                 double* shader_ghz) {
+  if (kernel < 0 || kernel > 2) return fail(kEinval, "kernel=%d must be 0 (forward), 1 (dK/dV) or 2 (dQ)", kernel);
+  return run_probe(3 + kernel, iters, seed, tflops, shader_ghz);
 }
 
 }  // extern "C"

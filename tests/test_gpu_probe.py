@@ -40,3 +40,24 @@ def test_probe_mfma_lds_rate_is_plausible(softmax):
 def test_probe_lds_rejects_bad_arguments():
     with pytest.raises(RuntimeError, match="iters"):
         _lib.probe_mfma_lds_rate(False, 17, 1)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kernel", ["fwd", "dkdv", "dq"])
+def test_probe_kernel_mix_is_plausible(kernel):
+    torch.cuda.init()
+    tf, ghz = _lib.probe_kernel_mix(kernel, 2052, 3407)
+    print(f"{kernel} instruction mix {tf:.1f} TFLOP/s at {ghz:.3f} GHz", flush=True)
+    assert 0.1 * PEAK_BF16_TFLOPS < tf <= 1.02 * PEAK_BF16_TFLOPS
+    assert 0.5 < ghz < 3.0
+
+
+@pytest.mark.gpu
+def test_probe_kernel_mix_rejects_bad_arguments():
+    lib = _lib.load_probe()
+    import ctypes
+    tf, ghz = ctypes.c_double(), ctypes.c_double()
+    assert lib.harp_probe_kernel_mix(3, 2052, 1, ctypes.byref(tf), ctypes.byref(ghz)) == 1
+    assert b"kernel" in lib.harp_probe_last_error()
+    with pytest.raises(RuntimeError, match="iters"):
+        _lib.probe_kernel_mix("dq", 15, 1)
