@@ -149,4 +149,75 @@ __device__ __forceinline__ void settle(float& x) { asm volatile("" : "+v"(x)); }
 // Scheduling fence: the compiler may not move any instruction across it.
 __device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
 
+// XOR swizzle of 16-byte chunks within a 256-byte LDS row: a permutation
+// of the 16 chunk positions for any 16 consecutive rows.
+__device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+
+// Max / sum of a value over the two halves of the wave (lanes l and l ^ 32).
+__device__ __forceinline__ float wave_half_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float wave_half_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Block index -> (tile, head, batch) with all tiles of one (b, h) kept on one
+// XCD (workgroups are dealt to the 8 XCDs round-robin), so a head's streamed
+// operands are fetched into that XCD's L2 once for all of its tiles.
+__device__ __forceinline__ void decode_block(int n_tiles, int H, int& tile, int& h, int& b) {
+  const int total = (int)gridDim.x;
+  int lin = (int)blockIdx.x;
+  if (total % 8 == 0) lin = (lin % 8) * (total / 8) + lin / 8;
+  tile = lin % n_tiles;
+  const int bh = lin / n_tiles;
+  h = bh % H;
+  b = bh / H;
+}
+
+// Position of a streamed KV tile in the ring: ring step, first key, and the
+// visited chunk's valid length and K / V bases (offset to this (b, h)).  The
+// cursor lives in scalar registers, so moving to the next tile reads the
+// chunk table (kernel arguments: dependent scalar loads of ~200 cycles each)
+// only when it crosses into the next chunk, not on every tile.
+struct KvCursor {
+  int step, k0, len;
+  const bf16* k;
+  const bf16* v;
+};
+// first non-empty chunk from ring step `step` on, before step `end`
+// (step == end: past the end)
+__device__ __forceinline__ void kv_enter(const ChunkTable& ct, int64_t kvo, int step, int end, KvCursor& c) {
+  while (step < end && ct.len[ct.order[step]] == 0) ++step;
+  c.step = step;
+  c.k0 = 0;
+  if (step < end) {
+    const int ch = ct.order[step];
+    c.len = ct.len[ch];
+    c.k = ct.k[ch] + kvo;
+    c.v = ct.v[ch] + kvo;
+  }
+}
+// the tile after the one of tile_keys keys at c
+__device__ __forceinline__ KvCursor kv_next(const ChunkTable& ct, int64_t kvo, const KvCursor& c, int tile_keys,
+                                             int end) {
+  KvCursor n = c;
+  n.k0 = c.k0 + tile_keys;
+  if (n.k0 >= c.len) kv_enter(ct, kvo, c.step + 1, end, n);
+  return n;
+}
+
+// KV split (grid dimension y): split s of n visits ring steps
+// [s * N / n, (s + 1) * N / n) and writes its results at offset s times the
+// split stride of its output buffers (the host points those at per-split
+// partial buffers; with n == 1 this is the whole ring and offset 0).
+struct KvSplit {
+  int begin, end, index;
+};
+__device__ __forceinline__ KvSplit kv_split(int n_chunks) {
+  const int s = (int)blockIdx.y, n = (int)gridDim.y;
+  return KvSplit{s * n_chunks / n, (s + 1) * n_chunks / n, s};
+}
+
 }  // namespace harp_ra

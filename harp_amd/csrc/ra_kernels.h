@@ -90,6 +90,10 @@ struct BwdParams {
 constexpr int kDkdvBlockKeys = 256;
 
 hipError_t launch_fwd(const FwdParams& p, hipStream_t st);
+// the forward with the hand-scheduled main loop (fwd_asm.hip), used by
+// launch_fwd where it applies
+bool fwd_asm_applies(const FwdParams& p);
+hipError_t launch_fwd_asm(const FwdParams& p, hipStream_t st);
 hipError_t launch_fwd_merge(const FwdMergeParams& p, hipStream_t st);
 hipError_t launch_dq_merge(const DqMergeParams& p, hipStream_t st);
 // Query rows per block of the forward and dQ kernels (the host sizes KV splits with it).
