@@ -9,14 +9,17 @@ wave's queries form two 32-query groups qg; every K / V fragment read from LDS
 feeds one MFMA per group (0.5 KB of LDS per MFMA).  Keys are streamed in
 32-key blocks J through eight 16 KiB LDS block buffers (K at 8 KiB * (J % 8),
 V at 64 KiB + 8 KiB * (J % 8)), copied global -> LDS by buffer_load ... lds
-six blocks ahead of their use.
+five blocks ahead of their use.  A barrier before every even slot J publishes
+blocks J + 1 and J + 2 and shows that every wave is done with slot J - 1, so
+the copies of slots J and J + 1 may go into the buffers of blocks J - 3 and
+J - 2.
 
-Slot J (one per key block, after a barrier):
+Slot J (one per key block):
   MFMAs  O(J-1) += V(J-1)^T P^T(J-1)   (a0..a127, 16 MFMAs)
          S(J+1)  = K(J+1) Q^T          (16 MFMAs, Q in a128..a191)
   VALU   online softmax of S(J): row max, lazy rescale check, P(J) = bf16 of
          exp2(S c2 - m), row sums (fp32, unrounded exps)
-  copies of block J + 6 (4 per wave)
+  copies of block J + 5 (4 per wave)
 The loop is unrolled over the eight buffers; each slot has a masked twin
 (keys past a chunk's valid length set to -inf) entered when its block is a
 chunk's partial last one, and a shared out-of-line rescale of O and l.
@@ -206,7 +209,7 @@ BUDGET = 20
 
 def slot_body(u, entry, masked):
     """The scheduled body of slot J (J % 8 == u): returns its Emitter."""
-    par, kbuf, vbuf, vnext, dmabuf = u % 2, (u + 1) % 8, (u + 7) % 8, u, (u + 6) % 8
+    par, kbuf, vbuf, vnext, dmabuf = u % 2, (u + 1) % 8, (u + 7) % 8, u, (u + 5) % 8
     em = Emitter.merged_entry(entry)
     mf, idx, pinned = [], {}, {}
     for p in PAIR_ORDER:
@@ -302,14 +305,14 @@ def prologue():
                  f"s_mov_b32 {s(STEP)}, %[step0]", f"s_mov_b32 {s(RING[0])}, 0", f"s_mov_b32 {s(RING[1])}, 0",
                  f"s_mov_b32 {s(J)}, 0", f"s_mov_b64 {s(FLAG, 2)}, 0"):
         em.raw(line, 1)
-    for b in range(6):
+    for b in range(5):
         for line in cursor_desc(b):
             em.raw(line, 1)
         for i in range(4):
             em.emit_all(dma(i, b))
         for line in cursor_adv(f"p{b}"):
             em.raw(line, 1)
-    em.raw("s_waitcnt vmcnt(20)")  # block 0 (this wave's part)
+    em.raw("s_waitcnt vmcnt(16)")  # block 0 (this wave's part)
     em.raw("s_barrier")
     mf = []
     for ks in range(8):
@@ -393,8 +396,9 @@ def build():
     lines += pro.lines
     lines.append(f"{lbl('loop')}:")
     for u in range(8):
-        lines += ["s_waitcnt vmcnt(16)", "s_barrier"]
-        lines += cursor_desc((u + 6) % 8)
+        if u % 2 == 0:
+            lines += ["s_waitcnt vmcnt(8)", "s_barrier"]
+        lines += cursor_desc((u + 5) % 8)
         lines.append(f"s_bfe_u32 {s(VALJ)}, {s(RING[u // 4])}, {hex(((u % 4) * 8) | (8 << 16))}")
         lines.append(f"s_cmp_lt_u32 {s(VALJ)}, 32")
         lines.append(f"s_cbranch_scc1 {lbl(f'mask{u}')}")
