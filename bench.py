@@ -436,6 +436,8 @@ def main() -> int:
     # the kernel's measured VALU / exp / copy work per MFMA, with nothing
     # waiting on anything -- the rate that mix allows on this board
     mix = {k: _lib.probe_kernel_mix(k, 24576, args.seed) for k in kernel_mfma}
+    if D == 128:  # the forward runs the hand-scheduled loop: its ceiling is that loop's steady state
+        mix["fwd"] = _lib.probe_fwd_asm_loop(4096, args.seed)
     kernels = {}
     for name, (ms, n) in kt.items():
         if n:

@@ -27,6 +27,12 @@
 //    Nothing in it depends on anything but its own registers: it is the rate
 //    that kernel's instruction mix allows on this board under its power
 //    limit, with no latency exposed and no wave waiting for another.
+// 5. harp_probe_fwd_asm_loop: the D = 128 forward's own generated loop
+//    (HARP_FWD_ASM_PROBE in fwd_asm.inc: the same instruction stream, with
+//    the copy cursor wrapping around one 1 MiB K and one 1 MiB V source of
+//    random bf16 instead of walking a chunk table), one 4-wave block per CU:
+//    the steady-state rate of that loop on this board, the ceiling of
+//    fwd_asm_kernel.
 // The board is power-limited under MFMA load: LDS reads and VALU work take
 // power from the MFMA stream, so mixes 2 and 3 run at a lower clock than 1.
 // They bound what a kernel with that operand path can reach, independently
@@ -40,6 +46,7 @@
 //   int harp_probe_mfma_rate(int iters, uint32_t seed, double* tflops, double* shader_ghz);
 //   int harp_probe_mfma_lds_rate(int iters, uint32_t seed, int softmax, double* tflops, double* shader_ghz);
 //   int harp_probe_kernel_mix(int kernel, int iters, uint32_t seed, double* tflops, double* shader_ghz);
+//   int harp_probe_fwd_asm_loop(int key_blocks, uint32_t seed, double* tflops, double* shader_ghz);
 //   const char* harp_probe_last_error(void);
 // Status 0 = ok, 1 = bad argument, 3 = allocation failed, 4 = launch failed.
 // Synchronous on the null stream; allocates and frees its own small buffers.
@@ -47,9 +54,12 @@
 #include <stdint.h>
 
 #include <cstdarg>
+#include <cstring>
 #include <cstdio>
 #include <string>
 #include <vector>
+
+#include "../fwd_asm.inc"
 
 namespace {
 
@@ -234,6 +244,88 @@ __global__ __launch_bounds__(64 * kLdsProbeWaves) void mfma_lds_probe_kernel(uin
   }
 }
 
+// Mix 5: the forward's generated loop on synthetic data (see the header).
+// Register tuples, LDS layout and per-lane addresses as fwd_asm_kernel sets
+// them up (fwd_asm.hip); keys are 1 MiB of K rows and 1 MiB of V rows
+// (4096 x 128 bf16 each), read 32 rows per block and wrapped around.
+typedef int v32i __attribute__((ext_vector_type(32)));
+constexpr int kFaSrcRows = 4096;
+__device__ __forceinline__ int fa_swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+
+__global__ __launch_bounds__(256, 1) void fwd_asm_probe_kernel(uint32_t seed, int nb, const uint16_t* kv, float c2,
+                                                              float* sink, long long* clocks) {
+  __shared__ __attribute__((aligned(16))) char lds[131072];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31, g = lane >> 5;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds;
+  {
+    uint4* vb7 = (uint4*)(lds + 65536 + 7 * 8192);
+    vb7[tid] = make_uint4(0u, 0u, 0u, 0u);
+    vb7[tid + 256] = make_uint4(0u, 0u, 0u, 0u);
+  }
+  v32i q0, q1;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const bf16x8 a = random_bf16x8(hash32(seed) ^ (blockIdx.x * 4096u + (uint32_t)tid * 16u + (uint32_t)k));
+    const bf16x8 b = random_bf16x8(hash32(seed) ^ (blockIdx.x * 4096u + (uint32_t)tid * 16u + 8u + (uint32_t)k));
+    const uint4 ua = __builtin_bit_cast(uint4, a), ub = __builtin_bit_cast(uint4, b);
+    q0[4 * k] = (int)ua.x, q0[4 * k + 1] = (int)ua.y, q0[4 * k + 2] = (int)ua.z, q0[4 * k + 3] = (int)ua.w;
+    q1[4 * k] = (int)ub.x, q1[4 * k + 1] = (int)ub.y, q1[4 * k + 2] = (int)ub.z, q1[4 * k + 3] = (int)ub.w;
+  }
+  asm volatile("" : "+{a[128:159]}"(q0), "+{a[160:191]}"(q1));
+  v32i misc, misc2;
+  {
+    int mv[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) mv[i] = 0;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) mv[ks] = (int)(lds0 + l32 * 256 + (((2 * ks + g) ^ fa_swz(l32)) << 4));
+    const int j = lane >> 4, sr = (lane >> 2) & 3, m = lane & 3;
+    const int cl = 2 * (j & 1) + (m >> 1);
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const int row = 8 * hh + 4 * g + sr;
+        mv[8 + hh * 4 + db] =
+            (int)(lds0 + 65536 + 2 * (row * 128 + (((4 * db + cl) ^ fa_swz(row)) << 3) + 4 * (m & 1)));
+      }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int r = (2 * wave + i) * 4 + (lane >> 4);
+      mv[16 + i] = r * 256 + (((lane & 15) ^ fa_swz(r)) << 4);
+    }
+    mv[18] = mv[19] = mv[20] = mv[21] = mv[26] = mv[27] = __float_as_int(-INFINITY);
+#pragma unroll
+    for (int i = 0; i < 32; ++i) misc[i] = mv[i];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) misc2[i] = 0;
+    misc2[1] = 4 * g;
+    misc2[2] = __float_as_int(-INFINITY);
+  }
+  asm volatile("" : "+{v[32:63]}"(misc), "+{v[192:223]}"(misc2));
+  v32i frag, pp, s0, s1, o0, o1, o2, o3;
+  const uint64_t kp0 = (uint64_t)(uintptr_t)kv, vp0 = kp0 + (uint64_t)kFaSrcRows * 256u;
+  const uint32_t dbase = lds0 + (uint32_t)wave * 2048u;
+  const long long t0 = clock64(), r0 = wall_clock64();
+  asm volatile(HARP_FWD_ASM_PROBE
+               : "+{v[32:63]}"(misc), "={v[64:95]}"(frag), "={v[96:127]}"(pp), "={v[128:159]}"(s0),
+                 "={v[160:191]}"(s1), "+{v[192:223]}"(misc2), "={a[0:31]}"(o0), "={a[32:63]}"(o1),
+                 "={a[64:95]}"(o2), "={a[96:127]}"(o3), "+{a[128:159]}"(q0), "+{a[160:191]}"(q1)
+               : [c2] "s"(c2), [dbase] "s"(dbase), [sbytes] "s"(256u), [blkb] "s"(8192u), [nb] "s"(nb),
+                 [kp0] "s"(kp0), [vp0] "s"(vp0), [left0] "s"(kFaSrcRows), [step0] "s"(0)
+               : "memory", "vcc", HARP_FWD_ASM_SGPR_CLOBBERS);
+  const long long t1 = clock64(), r1 = wall_clock64();
+  float acc = __int_as_float(misc[22]) + __int_as_float(misc[23]);
+#pragma unroll
+  for (int i = 0; i < 32; ++i) acc += __int_as_float(o0[i]) + __int_as_float(o3[i]);
+  sink[blockIdx.x * 256 + tid] = acc;
+  if (tid == 0) {
+    clocks[2 * blockIdx.x] = t1 - t0;
+    clocks[2 * blockIdx.x + 1] = r1 - r0;
+  }
+}
+
 thread_local std::string g_last_error;
 
 int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
@@ -278,6 +370,10 @@ int launch_mix(int mix, int blocks, int threads, uint32_t sd, int iters, float* 
     case 4:  // dK/dV: 2.5 VALU (0.5 exp), a copy per 16 MFMAs
       hipLaunchKernelGGL((mfma_lds_probe_kernel<2, 6, 2, 6, 2, 7, 4>), g, t, 0, nullptr, sd, iters, sink, clocks, src);
       break;
+    case 6:  // the forward's generated loop: iters = 32-key blocks
+      hipLaunchKernelGGL(fwd_asm_probe_kernel, g, t, 0, nullptr, sd, iters, (const uint16_t*)src,
+                         0.08838834764f * 1.44269504f, sink, clocks);
+      break;
     default:  // dQ: 3.33 VALU (0.67 exp), a copy per 12 MFMAs
       hipLaunchKernelGGL((mfma_lds_probe_kernel<3, 9, 3, 9, 2, 9, 3>), g, t, 0, nullptr, sd, iters, sink, clocks,
                          src);
@@ -289,12 +385,12 @@ int launch_mix(int mix, int blocks, int threads, uint32_t sd, int iters, float* 
 int run_probe(int mix, int iters, uint32_t seed, double* tflops, double* shader_ghz) {
   if (!tflops || !shader_ghz) return fail(kEinval, "probe outputs are NULL");
   if (iters < 16 || iters > (1 << 20) || iters % 2) return fail(kEinval, "iters=%d must be even, in [16, 2^20]", iters);
-  if (mix > 0) iters = (iters + 5) / 6 * 6;  // the LDS-fed loops run six steps per iteration
+  if (mix > 0 && mix < 6) iters = (iters + 5) / 6 * 6;  // the LDS-fed loops run six steps per iteration
   int dev = 0, cus = 0, wall_khz = 0;
   if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) ||
       hipDeviceGetAttribute(&wall_khz, hipDeviceAttributeWallClockRate, dev) || cus < 1 || wall_khz < 1)
     return fail(kElaunch, "device query failed");
-  const int threads = mix == 0 ? 256 : 64 * kLdsProbeWaves;
+  const int threads = (mix == 0 || mix == 6) ? 256 : 64 * kLdsProbeWaves;
   const int waves_per_block = threads / 64;
   const int blocks = mix == 0 ? 8 * cus : cus;  // 32 or 8 waves per CU
   float* sink = nullptr;
@@ -306,15 +402,23 @@ int run_probe(int mix, int iters, uint32_t seed, double* tflops, double* shader_
   float best_ms = 0.f;
   if (hipMalloc(&sink, sizeof(float) * threads * (size_t)blocks) != hipSuccess ||
       hipMalloc(&clocks, sizeof(long long) * 2 * (size_t)blocks) != hipSuccess ||
-      hipMalloc(&src, kCopySrcBytes) != hipSuccess) {
+      hipMalloc(&src, 2 * kCopySrcBytes) != hipSuccess) {
     rc = fail(kEnomem, "probe buffers: hipMalloc failed");
   } else if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
     rc = fail(kElaunch, "probe events: hipEventCreate failed");
   } else {
     // the copies' source: random bytes, so their data path toggles like real data
-    std::vector<uint32_t> r(kCopySrcBytes / 4);
+    std::vector<uint32_t> r(2 * kCopySrcBytes / 4);
     for (size_t i = 0; i < r.size(); ++i) r[i] = (uint32_t)(i * 2654435761u) ^ (seed * 0x9e3779b9u) ^ (uint32_t)(i >> 7);
-    if (hipMemcpy(src, r.data(), kCopySrcBytes, hipMemcpyHostToDevice) != hipSuccess)
+    if (mix == 6) {  // finite bf16 keys and values in [-1.7, 1.7]: pairs of (sign, exponent 117-127, mantissa)
+      for (size_t i = 0; i < r.size(); ++i) {
+        const uint32_t h = r[i] * 0x85ebca6bu;
+        const uint32_t lo = (h & 0x807fu) | ((117u + (h >> 7) % 11u) << 7);
+        const uint32_t hi = ((h >> 16) & 0x807fu) | ((117u + (h >> 23) % 11u) << 7);
+        r[i] = lo | (hi << 16);
+      }
+    }
+    if (hipMemcpy(src, r.data(), 2 * kCopySrcBytes, hipMemcpyHostToDevice) != hipSuccess)
       rc = fail(kElaunch, "probe copy source upload failed");
     // one warm-up launch (clocks ramp), then the timed one
     for (int rep = 0; rep < 2 && rc == kOk; ++rep) {
@@ -334,7 +438,8 @@ int run_probe(int mix, int iters, uint32_t seed, double* tflops, double* shader_
       shader += (double)h[2 * i];
       wall += (double)h[2 * i + 1];
     }
-    const double flop = (double)blocks * waves_per_block * 4.0 * iters * 32.0 * 32.0 * 16.0 * 2.0;
+    // mixes 0-5: four MFMAs per wave and step; mix 6: 32 per wave and key block
+    const double flop = (double)blocks * waves_per_block * (mix == 6 ? 32.0 : 4.0) * iters * 32.0 * 32.0 * 16.0 * 2.0;
     *tflops = (best_ms > 0.f) ? flop / (best_ms * 1e-3) / 1e12 : 0.0;
     *shader_ghz = (wall > 0.0) ? shader / wall * wall_khz * 1e-6 : 0.0;
   }
@@ -361,6 +466,11 @@ __attribute__((visibility("default"))) int harp_probe_mfma_lds_rate(int iters, u
                                                                     double* tflops, double* shader_ghz) {
   if (softmax != 0 && softmax != 1) return fail(kEinval, "softmax=%d must be 0 or 1", softmax);
   return run_probe(1 + softmax, iters, seed, tflops, shader_ghz);
+}
+
+__attribute__((visibility("default"))) int harp_probe_fwd_asm_loop(int key_blocks, uint32_t seed, double* tflops,
+                                                                   double* shader_ghz) {
+  return run_probe(6, key_blocks, seed, tflops, shader_ghz);
 }
 
 __attribute__((visibility("default"))) int harp_probe_kernel_mix(int kernel, int iters, uint32_t seed, double* tflops,

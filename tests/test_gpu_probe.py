@@ -61,3 +61,13 @@ def test_probe_kernel_mix_rejects_bad_arguments():
     assert b"kernel" in lib.harp_probe_last_error()
     with pytest.raises(RuntimeError, match="iters"):
         _lib.probe_kernel_mix("dq", 15, 1)
+
+
+@pytest.mark.gpu
+def test_probe_fwd_asm_loop_is_plausible():
+    """The D = 128 forward's generated loop on synthetic keys."""
+    torch.cuda.init()
+    tf, ghz = _lib.probe_fwd_asm_loop(256, 3407)
+    print(f"forward loop {tf:.1f} TFLOP/s at {ghz:.3f} GHz", flush=True)
+    assert 0.1 * PEAK_BF16_TFLOPS < tf <= 1.02 * PEAK_BF16_TFLOPS
+    assert 0.5 < ghz < 3.0
