@@ -47,6 +47,7 @@ LEFT, STEP, CH, T0, T1, VAL, VALJ, RING, J, U = 84, 85, 86, 87, 88, 90, 91, (92,
 SGPR_CLOBBER = list(range(60, 96))
 
 NEG_BIG = "0xff7fffff"  # -FLT_MAX
+SKEW_EXP, SKEW_ADD = 4, 8  # softmax pipeline: element k's exp and sum trail its FMA by this many elements
 TAU = "0x41000000"      # 8.0: lazy-rescale threshold (log2 units)
 
 
@@ -188,13 +189,13 @@ def softmax(par, masked):
             cvts[(qg, r)] = ins(f"v_cvt_pk_bf16_f32 {dst}, {sv(qg, r - 1)}, {sv(qg, r)}", "valu", dst=dst,
                                 src=f"{sv(qg, r - 1)} {sv(qg, r)}")
     n = len(order)
-    for k in range(n + 6):  # skewed: fma(k), exp(k - 2), add / cvt(k - 4)
+    for k in range(n + SKEW_ADD + 2):  # skewed: fma(k), exp(k - SKEW_EXP), add / cvt(k - SKEW_ADD)
         if k < n:
             L.append(fmas[order[k]])
-        if 0 <= k - 2 < n:
-            L.append(exps[order[k - 2]])
-        if 0 <= k - 4 < n:
-            e = order[k - 4]
+        if 0 <= k - SKEW_EXP < n:
+            L.append(exps[order[k - SKEW_EXP]])
+        if 0 <= k - SKEW_ADD < n:
+            e = order[k - SKEW_ADD]
             if e in adds:
                 L.append(adds[e])
             if e in cvts:
