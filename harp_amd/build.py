@@ -36,10 +36,10 @@ OPS_LIB = OUT / "libring_attention_ops.so"
 ASYNC_OPS_LIB = OUT / "libharp_async_op.so"
 PROBE_LIB = OUT / "libharp_probe.so"
 
-HIP_SOURCES = ["ra_kernels.hip", "fwd_asm.hip", "ra_abi.hip", "qk_kernels.hip", "qk_abi.hip", "proj_kernels.hip"]
+HIP_SOURCES = ["ra_kernels.hip", "fwd_asm.hip", "dq_asm.hip", "ra_abi.hip", "qk_kernels.hip", "qk_abi.hip", "proj_kernels.hip"]
 PROBE_SOURCE = "bench/mfma_probe.hip"
 HIP_HEADERS = ["ra_common.h", "ra_kernels.h", "qk_kernels.h", "proj_kernels.h", "fwd_asm.inc", "fwd_asm_gen.py",
-               "asm_sched.py"]
+               "dq_asm.inc", "dq_asm_gen.py", "asm_sched.py"]
 OPS_SOURCE = "torch_ring_attention_ops.cpp"
 ASYNC_OPS_SOURCE = "torch_async_op.cpp"
 
@@ -80,11 +80,11 @@ def _run(cmd: list[str], verbose: bool) -> None:
         print(out)
 
 
-def generate_asm(verbose: bool = False) -> Path:
-    """csrc/fwd_asm.inc: the hand-scheduled forward loop, from its generator."""
-    gen = CSRC / "fwd_asm_gen.py"
-    _run([sys.executable, str(gen)], verbose)
-    return CSRC / "fwd_asm.inc"
+def generate_asm(verbose: bool = False) -> None:
+    """csrc/fwd_asm.inc and dq_asm.inc: the hand-scheduled forward and dQ
+    loops, from their generators."""
+    for gen in ("fwd_asm_gen.py", "dq_asm_gen.py"):
+        _run([sys.executable, str(CSRC / gen)], verbose)
 
 
 def build_abi(verbose: bool = False) -> Path:

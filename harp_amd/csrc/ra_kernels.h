@@ -101,6 +101,10 @@ constexpr int kQueryBlockRows = 256;
 hipError_t launch_delta(const DeltaParams& p, hipStream_t st);
 hipError_t launch_stats_prep(const BwdParams& p, hipStream_t st);
 hipError_t launch_dq(const BwdParams& p, hipStream_t st);
+// the dQ kernel with the hand-scheduled main loop (dq_asm.hip), used by
+// launch_dq where it applies
+bool dq_asm_applies(const BwdParams& p);
+hipError_t launch_dq_asm(const BwdParams& p, hipStream_t st);
 hipError_t launch_dkdv(const BwdParams& p, hipStream_t st);
 
 }  // namespace harp_ra

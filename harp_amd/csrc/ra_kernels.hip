@@ -1125,7 +1125,10 @@ hipError_t launch_delta(const DeltaParams& p, hipStream_t st) {
   hipLaunchKernelGGL(delta_kernel, grid, dim3(256), 0, st, p);
   return hipGetLastError();
 }
-hipError_t launch_dq(const BwdParams& p, hipStream_t st) { HARP_RA_DISPATCH_D(p.D, launch_dq_t, p, st) }
+hipError_t launch_dq(const BwdParams& p, hipStream_t st) {
+  if (dq_asm_applies(p)) return launch_dq_asm(p, st);
+  HARP_RA_DISPATCH_D(p.D, launch_dq_t, p, st)
+}
 hipError_t launch_dkdv(const BwdParams& p, hipStream_t st) { HARP_RA_DISPATCH_D(p.D, launch_dkdv_t, p, st) }
 
 }  // namespace harp_ra
