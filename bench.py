@@ -32,7 +32,7 @@ PEAK_HBM_GBS = 8000.0
 # with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE, each scaled by what the same
 # counter reads for a 1 GiB device copy in the same run (FETCH x2.0, WRITE
 # x1.0).  Source: profiles/ring_attn_config4_counters.md.
-MEASURED_TRAFFIC_BYTES = {4: {"fwd": 960.0e6, "dkdv": 2518.9e6, "dq": 958.9e6, "delta": 151.8e6, "stats": 3.6e6}}
+MEASURED_TRAFFIC_BYTES = {4: {"fwd": 960.2e6, "dkdv": 2512.0e6, "dq": 959.4e6, "delta": 151.8e6, "stats": 3.6e6}}
 
 CONFIGS = {
     1: dict(B=1, H=8, T=512, D=64, N=1, tc=512, lens=None, vscale=1.0),
@@ -436,8 +436,9 @@ def main() -> int:
     # the kernel's measured VALU / exp / copy work per MFMA, with nothing
     # waiting on anything -- the rate that mix allows on this board
     mix = {k: _lib.probe_kernel_mix(k, 24576, args.seed) for k in kernel_mfma}
-    if D == 128:  # the forward runs the hand-scheduled loop: its ceiling is that loop's steady state
+    if D == 128:  # the forward and dQ run hand-scheduled loops: their ceilings are those loops' steady states
         mix["fwd"] = _lib.probe_fwd_asm_loop(4096, args.seed)
+        mix["dq"] = _lib.probe_dq_asm_loop(4096, args.seed)
     kernels = {}
     for name, (ms, n) in kt.items():
         if n:

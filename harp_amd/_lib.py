@@ -203,6 +203,9 @@ def load_probe() -> ctypes.CDLL:
             lib.harp_probe_fwd_asm_loop.restype = _i
             lib.harp_probe_fwd_asm_loop.argtypes = [_i, ctypes.c_uint32, ctypes.POINTER(ctypes.c_double),
                                                     ctypes.POINTER(ctypes.c_double)]
+            lib.harp_probe_dq_asm_loop.restype = _i
+            lib.harp_probe_dq_asm_loop.argtypes = [_i, ctypes.c_uint32, ctypes.POINTER(ctypes.c_double),
+                                                   ctypes.POINTER(ctypes.c_double)]
             lib.harp_probe_last_error.restype = ctypes.c_char_p
             lib.harp_probe_last_error.argtypes = []
             _probe = lib
@@ -265,6 +268,19 @@ def probe_fwd_asm_loop(key_blocks: int = 4096, seed: int = 3407) -> tuple:
     rc = lib.harp_probe_fwd_asm_loop(int(key_blocks), int(seed) & 0xFFFFFFFF, ctypes.byref(tf), ctypes.byref(ghz))
     if rc != 0:
         raise RuntimeError(f"harp_probe_fwd_asm_loop failed (status {rc}): {lib.harp_probe_last_error().decode()}")
+    return tf.value, ghz.value
+
+
+def probe_dq_asm_loop(key_blocks: int = 4096, seed: int = 3407) -> tuple:
+    """(TFLOP/s, shader GHz) of the D = 128 dQ kernel's own generated loop
+    (dq_asm.inc) run on synthetic keys for `key_blocks` 32-key blocks, one
+    4-wave block per CU: the steady-state ceiling of dq_asm_kernel."""
+    lib = load_probe()
+    tf = ctypes.c_double()
+    ghz = ctypes.c_double()
+    rc = lib.harp_probe_dq_asm_loop(int(key_blocks), int(seed) & 0xFFFFFFFF, ctypes.byref(tf), ctypes.byref(ghz))
+    if rc != 0:
+        raise RuntimeError(f"harp_probe_dq_asm_loop failed (status {rc}): {lib.harp_probe_last_error().decode()}")
     return tf.value, ghz.value
 
 

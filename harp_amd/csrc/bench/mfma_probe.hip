@@ -33,6 +33,10 @@
 //    random bf16 instead of walking a chunk table), one 4-wave block per CU:
 //    the steady-state rate of that loop on this board, the ceiling of
 //    fwd_asm_kernel.
+// 6. harp_probe_dq_asm_loop: the same for the D = 128 dQ kernel's generated
+//    loop (HARP_DQ_ASM_PROBE in dq_asm.inc), with random Q and dO and
+//    per-query statistics of the size the headline shape has: the ceiling of
+//    dq_asm_kernel.
 // The board is power-limited under MFMA load: LDS reads and VALU work take
 // power from the MFMA stream, so mixes 2 and 3 run at a lower clock than 1.
 // They bound what a kernel with that operand path can reach, independently
@@ -47,6 +51,7 @@
 //   int harp_probe_mfma_lds_rate(int iters, uint32_t seed, int softmax, double* tflops, double* shader_ghz);
 //   int harp_probe_kernel_mix(int kernel, int iters, uint32_t seed, double* tflops, double* shader_ghz);
 //   int harp_probe_fwd_asm_loop(int key_blocks, uint32_t seed, double* tflops, double* shader_ghz);
+//   int harp_probe_dq_asm_loop(int key_blocks, uint32_t seed, double* tflops, double* shader_ghz);
 //   const char* harp_probe_last_error(void);
 // Status 0 = ok, 1 = bad argument, 3 = allocation failed, 4 = launch failed.
 // Synchronous on the null stream; allocates and frees its own small buffers.
@@ -59,6 +64,7 @@
 #include <string>
 #include <vector>
 
+#include "../dq_asm.inc"
 #include "../fwd_asm.inc"
 
 namespace {
@@ -326,6 +332,98 @@ __global__ __launch_bounds__(256, 1) void fwd_asm_probe_kernel(uint32_t seed, in
   }
 }
 
+// Register tuples, LDS layout and per-lane addresses as dq_asm_kernel sets
+// them up (dq_asm.hip); the same wrapped 1 MiB K and V sources as above.
+// LSE2 = 16 (the log2 row sum of 2^16 keys with scores of unit spread, so P
+// is about 2^-16 as at the headline shape) and D = 0.5.
+__global__ __launch_bounds__(256, 1) void dq_asm_probe_kernel(uint32_t seed, int nb, const uint16_t* kv, float c2,
+                                                             float* sink, long long* clocks) {
+  __shared__ __attribute__((aligned(16))) char lds[131072];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31, g = lane >> 5;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds;
+  {
+    uint4* kb7 = (uint4*)(lds + 7 * 8192);
+    kb7[tid] = make_uint4(0u, 0u, 0u, 0u);
+    kb7[tid + 256] = make_uint4(0u, 0u, 0u, 0u);
+  }
+  // random Q; dO from it by sign flips and swapped bf16 halves (operands
+  // that toggle like independent data, without a second generator's registers)
+  v32i q0, q1, g0, g1;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const uint32_t h = hash32(seed) ^ (blockIdx.x * 4096u + (uint32_t)tid * 16u + (uint32_t)k);
+    const uint4 ua = __builtin_bit_cast(uint4, random_bf16x8(h)), ub = __builtin_bit_cast(uint4, random_bf16x8(h + 8u));
+    q0[4 * k] = (int)ua.x, q0[4 * k + 1] = (int)ua.y, q0[4 * k + 2] = (int)ua.z, q0[4 * k + 3] = (int)ua.w;
+    q1[4 * k] = (int)ub.x, q1[4 * k + 1] = (int)ub.y, q1[4 * k + 2] = (int)ub.z, q1[4 * k + 3] = (int)ub.w;
+  }
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    g0[i] = (int)((uint32_t)q1[i] ^ 0x80008000u);
+    g1[i] = (int)(((uint32_t)q0[i] >> 16) | ((uint32_t)q0[i] << 16));
+  }
+  asm volatile("" : "+{a[128:159]}"(q0), "+{a[160:191]}"(q1), "+{a[192:223]}"(g0), "+{a[224:255]}"(g1));
+  v32i misc;
+  {
+    int mv[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) mv[i] = 0;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      mv[ks] = (int)(lds0 + l32 * 256 + (((2 * ks + g) ^ fa_swz(l32)) << 4));
+      mv[8 + ks] = mv[ks] + 65536;
+    }
+    const int j = lane >> 4, sr = (lane >> 2) & 3, m = lane & 3;
+    const int cl = 2 * (j & 1) + (m >> 1);
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const int row = 8 * hh + 4 * g + sr;
+        mv[16 + hh * 4 + db] = (int)(lds0 + 2 * (row * 128 + (((4 * db + cl) ^ fa_swz(row)) << 3) + 4 * (m & 1)));
+      }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int r = (2 * wave + i) * 4 + (lane >> 4);
+      mv[24 + i] = r * 256 + (((lane & 15) ^ fa_swz(r)) << 4);
+    }
+    mv[26] = mv[27] = __float_as_int(16.0f);
+    mv[28] = mv[29] = __float_as_int(0.5f);
+    // unused slots: a value the compiler cannot fold (known-zero elements get
+    // reused as constants after the loop, which keeps the whole tuple alive)
+    mv[30] = mv[31] = (int)seed;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) misc[i] = mv[i];
+  }
+  v32i fr0, fr1, s0, s1, d0, d1, o0, o1, o2, o3;
+  const uint64_t kp0 = (uint64_t)(uintptr_t)kv, vp0 = kp0 + (uint64_t)kFaSrcRows * 256u;
+  const uint32_t dbase = lds0 + (uint32_t)wave * 2048u;
+  const long long t0 = clock64(), r0 = wall_clock64();
+  asm volatile(HARP_DQ_ASM_PROBE
+               : "+{v[32:63]}"(misc), "={v[64:95]}"(fr0), "={v[96:127]}"(fr1), "={v[128:159]}"(s0),
+                 "={v[160:191]}"(s1), "={v[192:223]}"(d0), "={v[224:255]}"(d1), "={a[0:31]}"(o0),
+                 "={a[32:63]}"(o1), "={a[64:95]}"(o2), "={a[96:127]}"(o3), "+{a[128:159]}"(q0),
+                 "+{a[160:191]}"(q1), "+{a[192:223]}"(g0), "+{a[224:255]}"(g1)
+               : [c2] "s"(c2), [dbase] "s"(dbase), [sbytes] "s"(256u), [blkb] "s"(8192u), [nb] "s"(nb),
+                 [kp0] "s"(kp0), [vp0] "s"(vp0), [left0] "s"(kFaSrcRows), [step0] "s"(0)
+               : "memory", "vcc", HARP_DQ_ASM_SGPR_CLOBBERS);
+  const long long t1 = clock64(), r1 = wall_clock64();
+  float acc = 0.f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) acc += __int_as_float(o0[i]) + __int_as_float(o3[i]);
+  // the lane index read again: the loop statement binds v32..v255, so no
+  // per-lane value is kept across it
+  int lane_e;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane_e));
+  float* sk = sink;
+  asm volatile("" : "+s"(sk));  // the pointer stays scalar across the loop
+  sk[blockIdx.x * 256 + wave * 64 + lane_e] = acc;
+  if (wave == 0 && lane_e == 0) {
+    clocks[2 * blockIdx.x] = t1 - t0;
+    clocks[2 * blockIdx.x + 1] = r1 - r0;
+  }
+}
+
 thread_local std::string g_last_error;
 
 int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
@@ -374,6 +472,10 @@ int launch_mix(int mix, int blocks, int threads, uint32_t sd, int iters, float* 
       hipLaunchKernelGGL(fwd_asm_probe_kernel, g, t, 0, nullptr, sd, iters, (const uint16_t*)src,
                          0.08838834764f * 1.44269504f, sink, clocks);
       break;
+    case 7:  // the dQ kernel's generated loop: iters = 32-key blocks
+      hipLaunchKernelGGL(dq_asm_probe_kernel, g, t, 0, nullptr, sd, iters, (const uint16_t*)src,
+                         0.08838834764f * 1.44269504f, sink, clocks);
+      break;
     default:  // dQ: 3.33 VALU (0.67 exp), a copy per 12 MFMAs
       hipLaunchKernelGGL((mfma_lds_probe_kernel<3, 9, 3, 9, 2, 9, 3>), g, t, 0, nullptr, sd, iters, sink, clocks,
                          src);
@@ -390,7 +492,7 @@ int run_probe(int mix, int iters, uint32_t seed, double* tflops, double* shader_
   if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) ||
       hipDeviceGetAttribute(&wall_khz, hipDeviceAttributeWallClockRate, dev) || cus < 1 || wall_khz < 1)
     return fail(kElaunch, "device query failed");
-  const int threads = (mix == 0 || mix == 6) ? 256 : 64 * kLdsProbeWaves;
+  const int threads = (mix == 0 || mix >= 6) ? 256 : 64 * kLdsProbeWaves;
   const int waves_per_block = threads / 64;
   const int blocks = mix == 0 ? 8 * cus : cus;  // 32 or 8 waves per CU
   float* sink = nullptr;
@@ -410,7 +512,7 @@ int run_probe(int mix, int iters, uint32_t seed, double* tflops, double* shader_
     // the copies' source: random bytes, so their data path toggles like real data
     std::vector<uint32_t> r(2 * kCopySrcBytes / 4);
     for (size_t i = 0; i < r.size(); ++i) r[i] = (uint32_t)(i * 2654435761u) ^ (seed * 0x9e3779b9u) ^ (uint32_t)(i >> 7);
-    if (mix == 6) {  // finite bf16 keys and values in [-1.7, 1.7]: pairs of (sign, exponent 117-127, mantissa)
+    if (mix >= 6) {  // finite bf16 keys and values in [-1.7, 1.7]: pairs of (sign, exponent 117-127, mantissa)
       for (size_t i = 0; i < r.size(); ++i) {
         const uint32_t h = r[i] * 0x85ebca6bu;
         const uint32_t lo = (h & 0x807fu) | ((117u + (h >> 7) % 11u) << 7);
@@ -438,8 +540,10 @@ int run_probe(int mix, int iters, uint32_t seed, double* tflops, double* shader_
       shader += (double)h[2 * i];
       wall += (double)h[2 * i + 1];
     }
-    // mixes 0-5: four MFMAs per wave and step; mix 6: 32 per wave and key block
-    const double flop = (double)blocks * waves_per_block * (mix == 6 ? 32.0 : 4.0) * iters * 32.0 * 32.0 * 16.0 * 2.0;
+    // mixes 0-5: four MFMAs per wave and step; per wave and key block, mix 6:
+    // 32 (S, O), mix 7: 48 (S, dP, dQ)
+    const double per = mix == 6 ? 32.0 : (mix == 7 ? 48.0 : 4.0);
+    const double flop = (double)blocks * waves_per_block * per * iters * 32.0 * 32.0 * 16.0 * 2.0;
     *tflops = (best_ms > 0.f) ? flop / (best_ms * 1e-3) / 1e12 : 0.0;
     *shader_ghz = (wall > 0.0) ? shader / wall * wall_khz * 1e-6 : 0.0;
   }
@@ -471,6 +575,11 @@ __attribute__((visibility("default"))) int harp_probe_mfma_lds_rate(int iters, u
 __attribute__((visibility("default"))) int harp_probe_fwd_asm_loop(int key_blocks, uint32_t seed, double* tflops,
                                                                    double* shader_ghz) {
   return run_probe(6, key_blocks, seed, tflops, shader_ghz);
+}
+
+__attribute__((visibility("default"))) int harp_probe_dq_asm_loop(int key_blocks, uint32_t seed, double* tflops,
+                                                                  double* shader_ghz) {
+  return run_probe(7, key_blocks, seed, tflops, shader_ghz);
 }
 
 __attribute__((visibility("default"))) int harp_probe_kernel_mix(int kernel, int iters, uint32_t seed, double* tflops,
