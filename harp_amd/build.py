@@ -36,10 +36,11 @@ OPS_LIB = OUT / "libring_attention_ops.so"
 ASYNC_OPS_LIB = OUT / "libharp_async_op.so"
 PROBE_LIB = OUT / "libharp_probe.so"
 
-HIP_SOURCES = ["ra_kernels.hip", "fwd_asm.hip", "dq_asm.hip", "ra_abi.hip", "qk_kernels.hip", "qk_abi.hip", "proj_kernels.hip"]
+HIP_SOURCES = ["ra_kernels.hip", "fwd_asm.hip", "dq_asm.hip", "dkdv_asm.hip", "ra_abi.hip", "qk_kernels.hip", "qk_abi.hip", "proj_kernels.hip"]
 PROBE_SOURCE = "bench/mfma_probe.hip"
 HIP_HEADERS = ["ra_common.h", "ra_kernels.h", "qk_kernels.h", "proj_kernels.h", "fwd_asm.inc", "fwd_asm_gen.py",
-               "dq_asm.inc", "dq_asm_gen.py", "asm_sched.py"]
+               "dq_asm.inc", "dq_asm_gen.py", "dkdv_asm.inc",
+               "dkdv_asm_gen.py", "asm_sched.py"]
 OPS_SOURCE = "torch_ring_attention_ops.cpp"
 ASYNC_OPS_SOURCE = "torch_async_op.cpp"
 
@@ -81,9 +82,9 @@ def _run(cmd: list[str], verbose: bool) -> None:
 
 
 def generate_asm(verbose: bool = False) -> None:
-    """csrc/fwd_asm.inc and dq_asm.inc: the hand-scheduled forward and dQ
-    loops, from their generators."""
-    for gen in ("fwd_asm_gen.py", "dq_asm_gen.py"):
+    """csrc/fwd_asm.inc, dq_asm.inc and dkdv_asm.inc: the hand-scheduled
+    forward, dQ and dK/dV loops, from their generators."""
+    for gen in ("fwd_asm_gen.py", "dq_asm_gen.py", "dkdv_asm_gen.py"):
         _run([sys.executable, str(CSRC / gen)], verbose)
 
 

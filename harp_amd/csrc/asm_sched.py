@@ -167,17 +167,36 @@ class Emitter:
             self.emit(i)
 
 
-def fill_schedule(em, mfmas, fillers, budget=28, pinned=None):
+def fill_schedule(em, mfmas, fillers, budget=28, pinned=None, flush_war=False):
     """Issue `mfmas` in order.  Before MFMA k, the instructions pinned[k]
     (LDS prefetches, copies); after it, filler instructions in list order (a
     small lookahead may pass ones not yet hazard-ready, never one they depend
     on) for up to `budget` issue cycles, spread evenly over the gaps.
+    flush_war: before MFMA k, if it writes registers that a pending filler
+    allowed at k (not_before <= k) reads or writes, issue the allowed fillers
+    up to the last such one, in list order: the MFMA must not overwrite what
+    they still have to use.  (Fillers gated past k are work on the MFMA's
+    result and stay pending.)
     Returns the fillers left over."""
     fillers = list(fillers)
     n = len(mfmas)
     for k, m in enumerate(mfmas):
         for p in (pinned or {}).get(k, []):
             em.emit(p)
+        if flush_war and fillers:
+            md = set(m.dst)
+            last = -1
+            for j, f in enumerate(fillers):
+                if f.not_before <= k and md & (set(f.src) | set(f.dst) | set(f.srcC)):
+                    last = j
+            if last >= 0:
+                keep = []
+                for f in fillers[:last + 1]:
+                    if f.not_before <= k:
+                        em.emit(f)
+                    else:
+                        keep.append(f)
+                fillers = keep + fillers[last + 1:]
         em.emit(m)
         left = sum(f.cost for f in fillers)
         target = min(budget, left / max(n - k, 1) + 2)

@@ -66,6 +66,20 @@ __device__ __forceinline__ bf16x8 zero8() {
 // Lane index computed anew (v_mbcnt) in an asm the compiler cannot merge with
 // an earlier one: an epilogue that derives its lane-dependent indices from it
 // keeps no such value live (or spilled) across the main loop.
+// A wave-uniform 32-bit value in an SGPR, for an inline-asm "s" operand.  A
+// value the compiler knows to be uniform but computes with VALU instructions
+// (a float product, say) is otherwise handed to an asm statement in a VGPR
+// whatever the constraint, and the assembler accepts that wherever only VALU
+// instructions read the operand.  The volatile readfirstlane cannot be folded.
+// The compiler's hazard pass does not look into the statement, so it waits
+// itself: v_readfirstlane right after the VALU write of its source reads the
+// old value (measured: without the wait some waves saw the multiplicand).
+__device__ __forceinline__ uint32_t sgpr_of(float x) {
+  uint32_t r;
+  asm volatile("s_nop 4\n\tv_readfirstlane_b32 %0, %1" : "=s"(r) : "v"(x));
+  return r;
+}
+
 __device__ __forceinline__ int lane_id_fresh() {
   int l;
   asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));

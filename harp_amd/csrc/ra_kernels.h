@@ -106,5 +106,9 @@ hipError_t launch_dq(const BwdParams& p, hipStream_t st);
 bool dq_asm_applies(const BwdParams& p);
 hipError_t launch_dq_asm(const BwdParams& p, hipStream_t st);
 hipError_t launch_dkdv(const BwdParams& p, hipStream_t st);
+// the dK/dV kernel with the hand-scheduled main loop (dkdv_asm.hip), used by
+// launch_dkdv where it applies
+bool dkdv_asm_applies(const BwdParams& p);
+hipError_t launch_dkdv_asm(const BwdParams& p, hipStream_t st);
 
 }  // namespace harp_ra

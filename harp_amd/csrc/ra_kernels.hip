@@ -1129,6 +1129,9 @@ hipError_t launch_dq(const BwdParams& p, hipStream_t st) {
   if (dq_asm_applies(p)) return launch_dq_asm(p, st);
   HARP_RA_DISPATCH_D(p.D, launch_dq_t, p, st)
 }
-hipError_t launch_dkdv(const BwdParams& p, hipStream_t st) { HARP_RA_DISPATCH_D(p.D, launch_dkdv_t, p, st) }
+hipError_t launch_dkdv(const BwdParams& p, hipStream_t st) {
+  if (dkdv_asm_applies(p)) return launch_dkdv_asm(p, st);
+  HARP_RA_DISPATCH_D(p.D, launch_dkdv_t, p, st)
+}
 
 }  // namespace harp_ra

@@ -1,0 +1,88 @@
+"""GPU parity of the head-dim-128 dK/dV kernel (dkdv_asm.hip, the
+hand-scheduled loop) on the paths its loop takes rarely: every exit point of
+the loop unrolled over five LDS buffers (1-11 query blocks of 32), a ragged
+last query block (rows past T load as zero), key blocks that are partly or
+wholly past a chunk's valid length (pad keys written as zero, blocks without
+a valid key skipping the loop), empty chunks, fp32 outputs, and a head-major
+dO.  Bars as the other parity tests: dQ, dK, dV <= 3e-2 relative Frobenius
+error against the fp64 oracle (oracle/ring_attn_oracle.py,
+ring_attn.cpp:2577-2829); pad keys' dK / dV exactly 0.
+"""
+
+import math
+
+import pytest
+import torch
+
+from oracle import ring_attn_oracle as orc
+from tests.gpu_harness import run_hip
+from tests.parity import TOL_GRAD, rel_fro
+from tests.test_gpu_parity import _check_all, _oracle_full
+
+pytestmark = pytest.mark.gpu
+
+D = 128
+
+
+def _grad_check(res, ref):
+    for name in ("dq", "dk", "dv"):
+        err = rel_fro(res[name], ref[name])
+        print(f"  {name}: rel {err:.2e}", flush=True)
+        assert err <= TOL_GRAD, (name, err)
+
+
+@pytest.mark.parametrize("T", [32, 64, 96, 128, 160, 192, 224, 256, 288, 330, 352])
+def test_every_loop_exit(T):
+    """One chunk of 300 keys (two 256-key blocks, the second mostly pads):
+    the loop runs ceil(T / 32) query blocks and leaves from slot
+    (nb - 1) % 5; T = 330 ends in a partial block."""
+    print(f"[dkdv exit T={T}]", flush=True)
+    q, ks, vs, do = orc.make_inputs(1, 2, T, D, 1, seed=300 + T, chunk_len=300)
+    scale = 1.0 / math.sqrt(D)
+    res = run_hip(q, ks, vs, do, scale)
+    ref = _oracle_full(q, ks, vs, do, scale)
+    _grad_check(res, ref)
+
+
+@pytest.mark.parametrize("grad_dtype", [torch.bfloat16, torch.float32])
+def test_pad_keys_and_empty_chunks(grad_dtype):
+    """Chunks of 1, 0, 257, 0, 511 and 300 valid keys (chunk length 520, so
+    every chunk has pad rows and some 256-key blocks hold no valid key) at
+    two ring ranks, through both entry points; pad rows must be exactly 0."""
+    lens = [1, 0, 257, 0, 511, 300]
+    tc = 520
+    for rank in (0, 3):
+        print(f"[dkdv pads rank {rank} {grad_dtype}]", flush=True)
+        q, ks, vs, do = orc.make_inputs(1, 2, 200, D, len(lens), seed=80 + rank, chunk_len=tc)
+        scale = 1.0 / math.sqrt(D)
+        res = run_hip(q, ks, vs, do, scale, ring_rank=rank, kv_lens=lens, grad_dtype=grad_dtype,
+                      via="abi" if rank else "ops")
+        ref = _oracle_full(q, ks, vs, do, scale, rank=rank, lens=lens)
+        _check_all(res, ref)
+        for ci, n in enumerate(lens):
+            for name in ("dk", "dv"):
+                pad = res[name][:, :, ci * tc + n:(ci + 1) * tc]
+                assert pad.numel() == 0 or torch.count_nonzero(pad) == 0, (name, ci)
+
+
+def test_head_major_grad_and_batch():
+    """Two batches, a head-major dO (other row strides than Q), ragged T."""
+    q, ks, vs, do = orc.make_inputs(2, 3, 171, D, 2, seed=21, chunk_len=384)
+    scale = 1.0 / math.sqrt(D)
+    res = run_hip(q, ks, vs, do, scale, do_layout="head")
+    ref = _oracle_full(q, ks, vs, do, scale)
+    _check_all(res, ref)
+
+
+def test_large_scores():
+    """Scores of a few hundred (scale 1): P is 0 for most keys and 1 at the
+    row maximum."""
+    g = torch.Generator().manual_seed(6)
+    B, H, T, tc = 1, 2, 100, 280
+    q = (2.0 * torch.randn((B, H, T, D), generator=g)).to(torch.bfloat16)
+    ks = [(2.0 * torch.randn((B, H, tc, D), generator=g)).to(torch.bfloat16) for _ in range(2)]
+    vs = [torch.randn((B, H, tc, D), generator=g).to(torch.bfloat16) for _ in range(2)]
+    do = torch.randn((B, H, T, D), generator=g).to(torch.bfloat16)
+    res = run_hip(q, ks, vs, do, 1.0)
+    ref = _oracle_full(q, ks, vs, do, 1.0)
+    _grad_check(res, ref)
