@@ -229,6 +229,7 @@ def s_part(gate):
 
 P2 = 32          # first phase-2 MFMA
 DMA_AT = (1, 7, 13, 19, 25, 29)
+SPLIT = 32       # the next block's first SPLIT exp-chain instructions run in this slot, the rest in the next
 
 
 def slot_body(u, entry):
@@ -265,7 +266,7 @@ def slot_body(u, entry):
     pin(P2 + 22, t_read(1))
     # RADDR to the next slot's S / dP buffer (block J + 2) after the last row read
     pin(P2 + 30, rebase(RADDR, (((u + 2) % NBUF) - rbuf) * BUF))
-    fillers = dp_part() + s_part(P2 + 16)
+    fillers = s_part(0)[SPLIT:] + dp_part() + s_part(P2 + 16)[:SPLIT]
     left = fill_schedule(em, mf_list, fillers, budget=BUDGET, pinned=pinned, flush_war=True)
     em.emit_all(left)
     return em
@@ -300,7 +301,7 @@ def prologue():
         pinned.setdefault(2 * (m - 2), []).extend(a_read(m))
     for ks in range(2, 8):
         pinned.setdefault(2 * (8 + ks - 1), []).extend(v_reads(ks))
-    left = fill_schedule(em, mfl, s_part(16), budget=BUDGET, pinned=pinned)
+    left = fill_schedule(em, mfl, s_part(16)[:SPLIT], budget=BUDGET, pinned=pinned)
     em.emit_all(left)
     # slot 0 reads S / dP rows from buffer 1; its dV / dK fragments (block -1,
     # zeros) from buffer 4, where TADDR starts
