@@ -436,9 +436,10 @@ def main() -> int:
     # the kernel's measured VALU / exp / copy work per MFMA, with nothing
     # waiting on anything -- the rate that mix allows on this board
     mix = {k: _lib.probe_kernel_mix(k, 24576, args.seed) for k in kernel_mfma}
-    if D == 128:  # the forward and dQ run hand-scheduled loops: their ceilings are those loops' steady states
+    if D == 128:  # the three kernels run hand-scheduled loops: their ceilings are those loops' steady states
         mix["fwd"] = _lib.probe_fwd_asm_loop(4096, args.seed)
         mix["dq"] = _lib.probe_dq_asm_loop(4096, args.seed)
+        mix["dkdv"] = _lib.probe_dkdv_asm_loop(4096, args.seed)
     kernels = {}
     for name, (ms, n) in kt.items():
         if n:

@@ -203,6 +203,9 @@ def load_probe() -> ctypes.CDLL:
             lib.harp_probe_fwd_asm_loop.restype = _i
             lib.harp_probe_fwd_asm_loop.argtypes = [_i, ctypes.c_uint32, ctypes.POINTER(ctypes.c_double),
                                                     ctypes.POINTER(ctypes.c_double)]
+            lib.harp_probe_dkdv_asm_loop.restype = _i
+            lib.harp_probe_dkdv_asm_loop.argtypes = [_i, ctypes.c_uint32, ctypes.POINTER(ctypes.c_double),
+                                                     ctypes.POINTER(ctypes.c_double)]
             lib.harp_probe_dq_asm_loop.restype = _i
             lib.harp_probe_dq_asm_loop.argtypes = [_i, ctypes.c_uint32, ctypes.POINTER(ctypes.c_double),
                                                    ctypes.POINTER(ctypes.c_double)]
@@ -281,6 +284,20 @@ def probe_dq_asm_loop(key_blocks: int = 4096, seed: int = 3407) -> tuple:
     rc = lib.harp_probe_dq_asm_loop(int(key_blocks), int(seed) & 0xFFFFFFFF, ctypes.byref(tf), ctypes.byref(ghz))
     if rc != 0:
         raise RuntimeError(f"harp_probe_dq_asm_loop failed (status {rc}): {lib.harp_probe_last_error().decode()}")
+    return tf.value, ghz.value
+
+
+def probe_dkdv_asm_loop(query_blocks: int = 4096, seed: int = 3407) -> tuple:
+    """(TFLOP/s, shader GHz) of the D = 128 dK/dV kernel's own generated loop
+    (dkdv_asm.inc) run on one synthetic query block for `query_blocks`
+    32-query blocks, one 4-wave block per CU: the steady-state ceiling of
+    dkdv_asm_kernel."""
+    lib = load_probe()
+    tf = ctypes.c_double()
+    ghz = ctypes.c_double()
+    rc = lib.harp_probe_dkdv_asm_loop(int(query_blocks), int(seed) & 0xFFFFFFFF, ctypes.byref(tf), ctypes.byref(ghz))
+    if rc != 0:
+        raise RuntimeError(f"harp_probe_dkdv_asm_loop failed (status {rc}): {lib.harp_probe_last_error().decode()}")
     return tf.value, ghz.value
 
 

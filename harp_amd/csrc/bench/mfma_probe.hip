@@ -37,6 +37,11 @@
 //    loop (HARP_DQ_ASM_PROBE in dq_asm.inc), with random Q and dO and
 //    per-query statistics of the size the headline shape has: the ceiling of
 //    dq_asm_kernel.
+// 7. harp_probe_dkdv_asm_loop: the same for the D = 128 dK/dV kernel's
+//    generated loop (HARP_DKDV_ASM_PROBE in dkdv_asm.inc: its copies re-read
+//    one 32-query block of random Q and dO), random K and V, statistics that
+//    put P near 2^-16 as at the headline shape: the ceiling of
+//    dkdv_asm_kernel.
 // The board is power-limited under MFMA load: LDS reads and VALU work take
 // power from the MFMA stream, so mixes 2 and 3 run at a lower clock than 1.
 // They bound what a kernel with that operand path can reach, independently
@@ -52,6 +57,7 @@
 //   int harp_probe_kernel_mix(int kernel, int iters, uint32_t seed, double* tflops, double* shader_ghz);
 //   int harp_probe_fwd_asm_loop(int key_blocks, uint32_t seed, double* tflops, double* shader_ghz);
 //   int harp_probe_dq_asm_loop(int key_blocks, uint32_t seed, double* tflops, double* shader_ghz);
+//   int harp_probe_dkdv_asm_loop(int query_blocks, uint32_t seed, double* tflops, double* shader_ghz);
 //   const char* harp_probe_last_error(void);
 // Status 0 = ok, 1 = bad argument, 3 = allocation failed, 4 = launch failed.
 // Synchronous on the null stream; allocates and frees its own small buffers.
@@ -64,6 +70,7 @@
 #include <string>
 #include <vector>
 
+#include "../dkdv_asm.inc"
 #include "../dq_asm.inc"
 #include "../fwd_asm.inc"
 
@@ -424,6 +431,98 @@ __global__ __launch_bounds__(256, 1) void dq_asm_probe_kernel(uint32_t seed, int
   }
 }
 
+// Register tuples, LDS layout and per-lane addresses as dkdv_asm_kernel sets
+// them up (dkdv_asm.hip): Q rows at the source's start, dO rows 1 MiB in, V
+// rows from 512 KiB in, the statistics planes (fp32, written by the host) in
+// its last 512 bytes; K from the per-lane hash.
+constexpr int kDkBuf = 16384, kDkVOff = 5 * kDkBuf, kDkVRow = 272, kDkStats = kDkVOff + 256 * kDkVRow;
+constexpr int kDkStatsPerWave = 5 * 512;
+__global__ __launch_bounds__(256, 1) void dkdv_asm_probe_kernel(uint32_t seed, int nb, const uint16_t* src,
+                                                               float c2, float* sink, long long* clocks) {
+  __shared__ __attribute__((aligned(16))) char lds[kDkStats + 4 * kDkStatsPerWave];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31, g = lane >> 5;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds;
+  {
+    const char* vsrc = (const char*)src + (512 << 10);
+#pragma unroll 4
+    for (int i = 0; i < 16; ++i) {
+      const int idx = i * 256 + tid, row = idx >> 4, ch = idx & 15;
+      *(uint4*)(lds + kDkVOff + row * kDkVRow + ch * 16) = *(const uint4*)(vsrc + row * 256 + ch * 16);
+    }
+    uint4* b4 = (uint4*)(lds + 4 * kDkBuf);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) b4[i * 256 + tid] = make_uint4(0u, 0u, 0u, 0u);
+  }
+  v32i kb0, kb1;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const uint32_t h = hash32(seed) ^ (blockIdx.x * 4096u + (uint32_t)tid * 16u + (uint32_t)k);
+    const uint4 ua = __builtin_bit_cast(uint4, random_bf16x8(h)), ub = __builtin_bit_cast(uint4, random_bf16x8(h + 8u));
+    kb0[4 * k] = (int)ua.x, kb0[4 * k + 1] = (int)ua.y, kb0[4 * k + 2] = (int)ua.z, kb0[4 * k + 3] = (int)ua.w;
+    kb1[4 * k] = (int)ub.x, kb1[4 * k + 1] = (int)ub.y, kb1[4 * k + 2] = (int)ub.z, kb1[4 * k + 3] = (int)ub.w;
+  }
+  __syncthreads();
+  v32i misc;
+  {
+    int mv[32];
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) mv[ks] = (int)(lds0 + l32 * 256 + (((2 * ks + g) ^ fa_swz(l32)) << 4));
+    const int j = lane >> 4, sr = (lane >> 2) & 3, m = lane & 3;
+    const int cl = 2 * (j & 1) + (m >> 1);
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const int row = 8 * hh + 4 * g + sr;
+        mv[8 + hh * 4 + db] =
+            (int)(lds0 + 4 * kDkBuf + 2 * (row * 128 + (((4 * db + cl) ^ fa_swz(row)) << 3) + 4 * (m & 1)));
+      }
+    mv[16] = (int)(lds0 + kDkVOff + (wave * 64 + l32) * kDkVRow + g * 16);
+    mv[17] = (int)(lds0 + kDkStats + wave * kDkStatsPerWave + g * 16);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int r = (2 * wave + i) * 4 + (lane >> 4);
+      mv[18 + i] = mv[20 + i] = r * 256 + (((lane & 15) ^ fa_swz(r)) << 4);
+    }
+    mv[22] = lane * 4;
+#pragma unroll
+    for (int i = 23; i < 32; ++i) mv[i] = mv[16];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) misc[i] = mv[i];
+  }
+  const uint64_t qp = (uint64_t)(uintptr_t)src, gp = qp + (1u << 20);
+  const uint64_t sp0 = qp + (2u << 20) - 512u, sp1 = sp0 + 256u;
+  const uint32_t dbase = lds0 + (uint32_t)wave * 2048u;
+  const uint32_t stb = lds0 + kDkStats + (uint32_t)wave * kDkStatsPerWave;
+  v32i sacc, dacc, pbds, init, frag, o0, o1, o2, o3, o4, o5, o6, o7;
+  const long long t0 = clock64(), r0 = wall_clock64();
+  asm volatile(HARP_DKDV_ASM_PROBE
+               : "+{v[0:31]}"(misc), "+{v[32:63]}"(kb0), "+{v[64:95]}"(kb1), "={v[96:127]}"(sacc),
+                 "={v[128:159]}"(dacc), "={v[160:191]}"(pbds), "={v[192:223]}"(init), "={v[224:255]}"(frag),
+                 "={a[0:31]}"(o0), "={a[32:63]}"(o1), "={a[64:95]}"(o2), "={a[96:127]}"(o3), "={a[128:159]}"(o4),
+                 "={a[160:191]}"(o5), "={a[192:223]}"(o6), "={a[224:255]}"(o7)
+               : [c2] "s"(__float_as_uint(c2)), [dbase] "s"(dbase), [sbase] "s"(stb), [qp] "s"(qp), [gp] "s"(gp),
+                 [sp0] "s"(sp0), [sp1] "s"(sp1), [qnr] "s"(8192u), [gnr] "s"(8192u), [snr] "s"(256u),
+                 [qstep] "s"(8192u), [gstep] "s"(8192u), [nb] "s"(nb)
+               : "memory", "vcc", HARP_DKDV_ASM_SGPR_CLOBBERS);
+  const long long t1 = clock64(), r1 = wall_clock64();
+  float acc = 0.f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) acc += __int_as_float(o0[i]) + __int_as_float(o7[i]);
+  // the lane index read again and the sink pointer kept scalar: the loop
+  // statement binds every VGPR
+  int lane_e;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane_e));
+  float* sk = sink;
+  asm volatile("" : "+s"(sk));
+  sk[blockIdx.x * 256 + wave * 64 + lane_e] = acc;
+  if (wave == 0 && lane_e == 0) {
+    clocks[2 * blockIdx.x] = t1 - t0;
+    clocks[2 * blockIdx.x + 1] = r1 - r0;
+  }
+}
+
 thread_local std::string g_last_error;
 
 int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
@@ -470,6 +569,10 @@ int launch_mix(int mix, int blocks, int threads, uint32_t sd, int iters, float* 
       break;
     case 6:  // the forward's generated loop: iters = 32-key blocks
       hipLaunchKernelGGL(fwd_asm_probe_kernel, g, t, 0, nullptr, sd, iters, (const uint16_t*)src,
+                         0.08838834764f * 1.44269504f, sink, clocks);
+      break;
+    case 8:  // the dK/dV kernel's generated loop: iters = 32-query blocks
+      hipLaunchKernelGGL(dkdv_asm_probe_kernel, g, t, 0, nullptr, sd, iters, (const uint16_t*)src,
                          0.08838834764f * 1.44269504f, sink, clocks);
       break;
     case 7:  // the dQ kernel's generated loop: iters = 32-key blocks
@@ -520,6 +623,14 @@ int run_probe(int mix, int iters, uint32_t seed, double* tflops, double* shader_
         r[i] = lo | (hi << 16);
       }
     }
+    if (mix == 8) {  // the dK/dV loop's statistics planes: S' c = S c - 16 (P near 2^-16), D = 0.5
+      const float c2 = 0.08838834764f * 1.44269504f, lse = -16.f / c2, dlt = -0.5f;
+      float* st = (float*)(r.data() + r.size() - 128);
+      for (int i = 0; i < 64; ++i) {
+        st[i] = lse;
+        st[64 + i] = dlt;
+      }
+    }
     if (hipMemcpy(src, r.data(), 2 * kCopySrcBytes, hipMemcpyHostToDevice) != hipSuccess)
       rc = fail(kElaunch, "probe copy source upload failed");
     // one warm-up launch (clocks ramp), then the timed one
@@ -542,7 +653,7 @@ int run_probe(int mix, int iters, uint32_t seed, double* tflops, double* shader_
     }
     // mixes 0-5: four MFMAs per wave and step; per wave and key block, mix 6:
     // 32 (S, O), mix 7: 48 (S, dP, dQ)
-    const double per = mix == 6 ? 32.0 : (mix == 7 ? 48.0 : 4.0);
+    const double per = mix == 6 ? 32.0 : (mix == 7 ? 48.0 : (mix == 8 ? 64.0 : 4.0));
     const double flop = (double)blocks * waves_per_block * per * iters * 32.0 * 32.0 * 16.0 * 2.0;
     *tflops = (best_ms > 0.f) ? flop / (best_ms * 1e-3) / 1e12 : 0.0;
     *shader_ghz = (wall > 0.0) ? shader / wall * wall_khz * 1e-6 : 0.0;
@@ -580,6 +691,11 @@ __attribute__((visibility("default"))) int harp_probe_fwd_asm_loop(int key_block
 __attribute__((visibility("default"))) int harp_probe_dq_asm_loop(int key_blocks, uint32_t seed, double* tflops,
                                                                   double* shader_ghz) {
   return run_probe(7, key_blocks, seed, tflops, shader_ghz);
+}
+
+__attribute__((visibility("default"))) int harp_probe_dkdv_asm_loop(int query_blocks, uint32_t seed, double* tflops,
+                                                                    double* shader_ghz) {
+  return run_probe(8, query_blocks, seed, tflops, shader_ghz);
 }
 
 __attribute__((visibility("default"))) int harp_probe_kernel_mix(int kernel, int iters, uint32_t seed, double* tflops,

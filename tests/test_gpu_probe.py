@@ -81,3 +81,13 @@ def test_probe_dq_asm_loop_is_plausible():
     print(f"dQ loop {tf:.1f} TFLOP/s at {ghz:.3f} GHz", flush=True)
     assert 0.1 * PEAK_BF16_TFLOPS < tf <= 1.02 * PEAK_BF16_TFLOPS
     assert 0.5 < ghz < 3.0
+
+
+@pytest.mark.gpu
+def test_probe_dkdv_asm_loop_is_plausible():
+    """The D = 128 dK/dV kernel's generated loop on one synthetic query block."""
+    torch.cuda.init()
+    tf, ghz = _lib.probe_dkdv_asm_loop(256, 3407)
+    print(f"dK/dV loop {tf:.1f} TFLOP/s at {ghz:.3f} GHz", flush=True)
+    assert 0.1 * PEAK_BF16_TFLOPS < tf <= 1.02 * PEAK_BF16_TFLOPS
+    assert 0.5 < ghz < 3.0
