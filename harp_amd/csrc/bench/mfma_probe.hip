@@ -395,7 +395,7 @@ __global__ __launch_bounds__(256, 1) void dq_asm_probe_kernel(uint32_t seed, int
       mv[24 + i] = r * 256 + (((lane & 15) ^ fa_swz(r)) << 4);
     }
     mv[26] = mv[27] = __float_as_int(16.0f);
-    mv[28] = mv[29] = __float_as_int(0.5f);
+    mv[28] = mv[29] = (int)seed;
     // unused slots: a value the compiler cannot fold (known-zero elements get
     // reused as constants after the loop, which keeps the whole tuple alive)
     mv[30] = mv[31] = (int)seed;
@@ -403,11 +403,16 @@ __global__ __launch_bounds__(256, 1) void dq_asm_probe_kernel(uint32_t seed, int
     for (int i = 0; i < 32; ++i) misc[i] = mv[i];
   }
   v32i fr0, fr1, s0, s1, d0, d1, o0, o1, o2, o3;
+  // -D = -0.5 for every query: the initial dP^T accumulators
+  v32i negd;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) negd[i] = __float_as_int(-0.5f);
   const uint64_t kp0 = (uint64_t)(uintptr_t)kv, vp0 = kp0 + (uint64_t)kFaSrcRows * 256u;
   const uint32_t dbase = lds0 + (uint32_t)wave * 2048u;
   const long long t0 = clock64(), r0 = wall_clock64();
   asm volatile(HARP_DQ_ASM_PROBE
-               : "+{v[32:63]}"(misc), "={v[64:95]}"(fr0), "={v[96:127]}"(fr1), "={v[128:159]}"(s0),
+               : "+{v[0:31]}"(negd), "+{v[32:63]}"(misc), "={v[64:95]}"(fr0), "={v[96:127]}"(fr1),
+                 "={v[128:159]}"(s0),
                  "={v[160:191]}"(s1), "={v[192:223]}"(d0), "={v[224:255]}"(d1), "={a[0:31]}"(o0),
                  "={a[32:63]}"(o1), "={a[64:95]}"(o2), "={a[96:127]}"(o3), "+{a[128:159]}"(q0),
                  "+{a[160:191]}"(q1), "+{a[192:223]}"(g0), "+{a[224:255]}"(g1)

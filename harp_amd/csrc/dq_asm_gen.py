@@ -13,7 +13,8 @@ copied five blocks ahead, with a barrier before every even slot.
 
 Slot J:
   MFMAs  dQ^T(J-1) += K^T(J-1) dS^T(J-1)  (16)
-         S^T(J+1) = K(J+1) Q^T, dP^T(J+1) = V(J+1) dO^T  (16 + 16)
+         S^T(J+1) = K(J+1) Q^T, dP^T(J+1) = V(J+1) dO^T - D  (16 + 16; the
+         dP^T accumulators start from -D of the lane's query, in v0..v31)
   VALU   P = exp2(S^T c2 - LSE2) clamped to [0, 1], dS^T = P (dP^T - D) of
          block J, rounded to bf16 after the dQ MFMAs have read the previous
          block's dS^T
@@ -33,7 +34,9 @@ from fwd_asm_gen import (DK, DV, FLAG, J, LEFT, RING, SGPR_CLOBBER, STEP, a, cur
 
 # ---- registers ------------------------------------------------------------
 KADDR, VADDR, TADDR, DOFF = 32, 40, 48, 56   # per-lane LDS addresses / copy offsets
-LSE, DLT = 58, 60                            # pairs (qg): LSE2 and D of the lane's query
+LSE = 58                                     # pair (qg): LSE2 of the lane's query
+NEGD = 0                                     # v0..v31: -D of the lane's query, 16 copies per qg (the
+                                             # initial dP^T accumulator, so dP - D needs no VALU)
 KF, VF, TF = 64, 80, 96                      # 4 fragment buffers x 4 registers each
 DS = 112                                     # dS^T bf16: qg * 8 + k2 * 4 + w
 S = (128, 160)                               # S^T[par]: qg * 16 + r
@@ -56,8 +59,9 @@ def mf_dp(ks, par):
     for qg in range(2):
         acc = v(DP[1 - par] + 16 * qg, 16)
         fr, b = v(VF + 4 * (ks % 4), 4), a(ADO + (qg * 8 + ks) * 4, 4)
-        out.append(ins(f"v_mfma_f32_32x32x16_bf16 {acc}, {fr}, {b}, {'0' if ks == 0 else acc}", "mfma", dst=acc,
-                       src=f"{fr} {b}", srcC=(acc if ks else "")))
+        c = v(NEGD + 16 * qg, 16) if ks == 0 else acc
+        out.append(ins(f"v_mfma_f32_32x32x16_bf16 {acc}, {fr}, {b}, {c}", "mfma", dst=acc, src=f"{fr} {b}",
+                       srcC=c))
     return out
 
 
@@ -104,8 +108,6 @@ def valu(par, gate):
     fma = {e: ins(f"v_fma_f32 {sv(*e)}, {sv(*e)}, %[c2], -{v(LSE + e[0])}", "valu", dst=sv(*e),
                   src=f"{sv(*e)} {v(LSE + e[0])}") for e in order}
     ex = {e: ins(f"v_exp_f32_e64 {sv(*e)}, {sv(*e)} clamp", "trans", dst=sv(*e), src=sv(*e)) for e in order}
-    sub = {e: ins(f"v_sub_f32_e32 {dv(*e)}, {dv(*e)}, {v(DLT + e[0])}", "valu", dst=dv(*e),
-                  src=f"{dv(*e)} {v(DLT + e[0])}") for e in order}
     mul = {e: ins(f"v_mul_f32_e32 {dv(*e)}, {sv(*e)}, {dv(*e)}", "valu", dst=dv(*e), src=f"{sv(*e)} {dv(*e)}")
            for e in order}
     cvt = []
@@ -119,10 +121,9 @@ def valu(par, gate):
             cvt.append((r, qg, c))
     L = []
     n = len(order)
-    for k in range(n + 8):  # skewed: fma / sub(k), exp(k - 2), mul(k - 4)
+    for k in range(n + 8):  # skewed: fma(k), exp(k - 2), mul(k - 4)
         if k < n:
             L.append(fma[order[k]])
-            L.append(sub[order[k]])
         if 0 <= k - 2 < n:
             L.append(ex[order[k - 2]])
         if 0 <= k - 4 < n:
