@@ -40,11 +40,12 @@ def _ring_step(q, k, v, do, N, out, m, l, dq, dk, dv):
     ops.ring_attention_backward(q, dq, k, dk, v, dv, do, m, l, D, N, scale)
 
 
-def test_ring_attention_graph_replays_equal_eager():
+@pytest.mark.parametrize("D", [64, 128])  # compiled kernels; the hand-scheduled D = 128 loops
+def test_ring_attention_graph_replays_equal_eager(D):
     harp_amd.load_ops()
     _lib.timing_enable(False)  # no per-launch timing events inside the capture
     N = 2
-    q, k, v, do = _inputs(0)
+    q, k, v, do = _inputs(0, D=D)
     out = torch.empty(q.shape, dtype=torch.float32, device=DEV)
     B, H, T, _ = q.shape
     m = torch.empty((B, H, T, 1), dtype=torch.bfloat16, device=DEV)
@@ -64,7 +65,7 @@ def test_ring_attention_graph_replays_equal_eager():
         _ring_step(q, k, v, do, N, *outs)
 
     for seed in (1, 2, 3):
-        nq, nk, nv, ndo = _inputs(seed)
+        nq, nk, nv, ndo = _inputs(seed, D=D)
         for dst, src in ((q, nq), (k, nk), (v, nv), (do, ndo)):
             dst.copy_(src)
         graph.replay()
