@@ -195,13 +195,18 @@ def test_config5_ragged_masked():
 
 # --- boundary semantics ----------------------------------------------------------
 
-def _small():
-    q, ks, vs, do = orc.make_inputs(1, 4, 200, 64, 3, seed=0, chunk_len=136)
-    return q, ks, vs, do, 0.125
+def _small(D=64):
+    q, ks, vs, do = orc.make_inputs(1, 4, 200, D, 3, seed=0, chunk_len=136)
+    return q, ks, vs, do, 1.0 / math.sqrt(D)
 
 
-def test_layouts_dtypes_and_paths_agree():
-    q, ks, vs, do, scale = _small()
+# D = 64 runs the compiled kernels, D = 128 the hand-scheduled loops
+SMALL_DIMS = pytest.mark.parametrize("D", [64, 128])
+
+
+@SMALL_DIMS
+def test_layouts_dtypes_and_paths_agree(D):
+    q, ks, vs, do, scale = _small(D)
     base = run_hip(q, ks, vs, do, scale)
     ref = _oracle_full(q, ks, vs, do, scale)
     _check_all(base, ref)
@@ -230,12 +235,13 @@ def test_layouts_dtypes_and_paths_agree():
                 assert same, (kw, key)
 
 
+@SMALL_DIMS
 @pytest.mark.parametrize("rank", [1, 2])
-def test_ring_rank_order(rank):
+def test_ring_rank_order(rank, D):
     """ring_rank changes the chunk visiting order; the result stays within the
     bar of the oracle, and differs from rank 0 only by bf16 rounding of P
     (the running max, the reference point of P, is reached in another order)."""
-    q, ks, vs, do, scale = _small()
+    q, ks, vs, do, scale = _small(D)
     ref = _oracle_full(q, ks, vs, do, scale, rank=rank)
     base = run_hip(q, ks, vs, do, scale)
     r = run_hip(q, ks, vs, do, scale, ring_rank=rank)
@@ -245,8 +251,9 @@ def test_ring_rank_order(rank):
     assert err_o < 5e-3 and err_lse < 1e-4, (err_o, err_lse)
 
 
-def test_bf16_m_is_lse_consistent():
-    q, ks, vs, do, scale = _small()
+@SMALL_DIMS
+def test_bf16_m_is_lse_consistent(D):
+    q, ks, vs, do, scale = _small(D)
     r16 = run_hip(q, ks, vs, do, scale, backward=False)
     r32 = run_hip(q, ks, vs, do, scale, m_dtype=torch.float32, backward=False)
     assert torch.equal(r16["m"].float(), r16["m"].float().bfloat16().float())
@@ -290,8 +297,9 @@ def test_very_negative_lse_with_pad_keys(via, D):
     _check_all(res, ref)
 
 
-def test_nan_propagates_to_its_row_only():
-    q, ks, vs, do, scale = _small()
+@SMALL_DIMS
+def test_nan_propagates_to_its_row_only(D):
+    q, ks, vs, do, scale = _small(D)
     q = q.clone()
     q[0, 1, 7, 3] = float("nan")
     res = run_hip(q, ks, vs, do, scale, backward=False)
