@@ -17,27 +17,36 @@ J - 2.
 Slot J (one per key block):
   MFMAs  O(J-1) += V(J-1)^T P^T(J-1)   (a0..a127, 16 MFMAs)
          S(J+1)  = K(J+1) Q^T          (16 MFMAs, Q in a128..a191)
-  VALU   online softmax of S(J): row max, lazy rescale check, P(J) = bf16 of
-         exp2(S c2 - m), row sums (fp32, unrounded exps)
+  VALU   online softmax of S(J): P(J) = bf16 of exp2(S c2 - m_ref) against
+         the lane's current reference point m_ref, row sums (fp32, unrounded
+         exps), the lane's running maximum of the raw scores, and the rescale
+         check: a lane whose 16 exps of the block sum above 2^8 (some key
+         above m_ref + 8 in log2 units, or the first keys of a row, whose
+         m_ref is still -FLT_MAX and whose exps overflow) flags the wave
   copies of block J + 5 (4 per wave)
 The loop is unrolled over the eight buffers; each slot has a masked twin
 (keys past a chunk's valid length set to -inf) entered when its block is a
-chunk's partial last one, and a shared out-of-line rescale of O and l.
+chunk's partial last one, and an out-of-line rescale (one per slot parity):
+m_ref moves to the row's running maximum (both lane halves), O and l are
+multiplied by 2^(old - new), and P(J) and the block sums are computed again
+from S(J), which the exps leave intact.  The exact row maximum is the lanes'
+running maxima, combined once by the kernel's epilogue.
 The reference math is ring_attn.cpp:2412-2575 (ring_attention_forward).
 """
 import os
 import sys
 
 sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
-from asm_sched import Emitter, fill_schedule, ins  # noqa: E402
+from asm_sched import Emitter, fill_schedule, ins, regs_of  # noqa: E402
 
 # ---- registers ------------------------------------------------------------
 KADDR, VADDR, DOFF = 32, 40, 48          # per-lane LDS addresses / copy offsets
-MREF, MMAX, LRUN, LSUM, MNEW, MX, MUSE = 50, 52, 54, 56, 58, 60, 62  # pairs (qg)
+MREF, MMAX, LRUN, LSUM, MNEW, MX = 50, 52, 54, 56, 58, 60  # pairs (qg)
 KF, VF = 64, 80                          # 4 fragment buffers x 4 registers each
 P = (96, 112)                            # P[par]: qg * 8 + k2 * 4 + w
 S = (128, 160)                           # S[par]: qg * 16 + r
 LIM, G4, NEGV, TMP, CORR = 192, 193, 194, 196, 204  # misc2 tuple v192..v223
+ET, NET = 206, 12                        # ring of exp temporaries v206..v217 (misc2)
 AQ = 128                                 # Q in a128..a191: (qg * 8 + ks) * 4
 # SGPRs (clobbered by the asm statement)
 F, FLAG, MK = (60, 62), 64, (66, 68)
@@ -48,7 +57,7 @@ SGPR_CLOBBER = list(range(60, 96))
 
 NEG_BIG = "0xff7fffff"  # -FLT_MAX
 SKEW_EXP, SKEW_ADD = 4, 8  # softmax pipeline: element k's exp and sum trail its FMA by this many elements
-TAU = "0x41000000"      # 8.0: lazy-rescale threshold (log2 units)
+LIMIT = "0x43800000"    # 256.0 = 2^8: a lane's block sum above it triggers the rescale
 
 
 def v(r, n=1):
@@ -118,8 +127,49 @@ def dma(i, dmabuf):
             ins(f"buffer_load_dwordx4 {v(DOFF + i % 2)}, {desc}, 0 offen lds", "vmem", src=[v(DOFF + i % 2), "m0"])]
 
 
-def softmax(par, masked):
+def exp_pipeline(par):
+    """P(par) = bf16 of exp2(S(par) c2 - m_ref) and the block sums LSUM, the
+    exps in the temporaries ET.. (S stays intact), skewed: fma(k),
+    exp(k - SKEW_EXP), add / pack(k - SKEW_ADD).  Element k's temporary is
+    last read by the pack of element k + 2, before element k + NET's fma."""
     cur, pn = S[par], P[par]
+    sv = lambda qg, r: v(cur + 16 * qg + r)
+    order = [(qg, r) for r in range(16) for qg in range(2)]
+    tv = {e: v(ET + k % NET) for k, e in enumerate(order)}
+    fmas = {e: ins(f"v_fma_f32 {tv[e]}, {sv(*e)}, %[c2], -{v(MREF + e[0])}", "valu", dst=tv[e],
+                   src=f"{sv(*e)} {v(MREF + e[0])}") for e in order}
+    exps = {e: ins(f"v_exp_f32_e32 {tv[e]}, {tv[e]}", "trans", dst=tv[e], src=tv[e]) for e in order}
+    adds, cvts = {}, {}
+    for (qg, r) in order:
+        if r == 1:
+            adds[(qg, r)] = ins(f"v_add_f32_e32 {v(LSUM + qg)}, {tv[(qg, 0)]}, {tv[(qg, 1)]}", "valu",
+                                dst=v(LSUM + qg), src=f"{tv[(qg, 0)]} {tv[(qg, 1)]}")
+        elif r > 1:
+            adds[(qg, r)] = ins(f"v_add_f32_e32 {v(LSUM + qg)}, {v(LSUM + qg)}, {tv[(qg, r)]}", "valu",
+                                dst=v(LSUM + qg), src=f"{v(LSUM + qg)} {tv[(qg, r)]}")
+        if r % 2 == 1:
+            k2, j = r // 8, (r - 1) % 8
+            dst = v(pn + qg * 8 + k2 * 4 + j // 2)
+            cvts[(qg, r)] = ins(f"v_cvt_pk_bf16_f32 {dst}, {tv[(qg, r - 1)]}, {tv[(qg, r)]}", "valu", dst=dst,
+                                src=f"{tv[(qg, r - 1)]} {tv[(qg, r)]}")
+    L = []
+    n = len(order)
+    for k in range(n + SKEW_ADD + 2):
+        if k < n:
+            L.append(fmas[order[k]])
+        if 0 <= k - SKEW_EXP < n:
+            L.append(exps[order[k - SKEW_EXP]])
+        if 0 <= k - SKEW_ADD < n:
+            e = order[k - SKEW_ADD]
+            if e in adds:
+                L.append(adds[e])
+            if e in cvts:
+                L.append(cvts[e])
+    return L
+
+
+def softmax(par, masked):
+    cur = S[par]
     L = []
     sv = lambda qg, r: v(cur + 16 * qg + r)
     for qg in range(2):  # the previous block's row sums (relative to the current reference)
@@ -132,74 +182,21 @@ def softmax(par, masked):
             for qg in range(2):
                 L.append(ins(f"v_cndmask_b32_e32 {sv(qg, r)}, {sv(qg, r)}, {v(NEGV)}, vcc", "valu", dst=sv(qg, r),
                              src=[*[sv(qg, r)], v(NEGV), "vcc"]))
-    for step in range(8):  # lane max over the 16 keys of each group
+    body = exp_pipeline(par)
+    # the lane's running maximum of the raw scores, between the pipeline's first instructions
+    mx = []
+    for step in range(8):
         for qg in range(2):
-            m = v(MX + qg)
-            if step == 0:
-                L.append(ins(f"v_max3_f32 {m}, {sv(qg, 0)}, {sv(qg, 1)}, {sv(qg, 2)}", "valu", dst=m,
-                             src=f"{sv(qg, 0)} {sv(qg, 1)} {sv(qg, 2)}"))
-            elif step < 7:
-                r0 = 1 + 2 * step
-                L.append(ins(f"v_max3_f32 {m}, {m}, {sv(qg, r0)}, {sv(qg, r0 + 1)}", "valu", dst=m,
-                             src=f"{m} {sv(qg, r0)} {sv(qg, r0 + 1)}"))
-            else:
-                L.append(ins(f"v_max_f32_e32 {m}, {m}, {sv(qg, 15)}", "valu", dst=m, src=f"{m} {sv(qg, 15)}"))
-    m0, m1 = v(MX), v(MX + 1)
-    # [mx0 lo | mx1 lo], [mx0 hi | mx1 hi] -> max -> [M0 | M1] -> copy, swap -> [M0 | M0], [M1 | M1]
-    L.append(ins(f"v_permlane32_swap_b32_e32 {m0}, {m1}", "perm", dst=f"{m0} {m1}", src=f"{m0} {m1}"))
-    L.append(ins(f"v_max_f32_e32 {m0}, {m0}, {m1}", "valu", dst=m0, src=f"{m0} {m1}"))
-    L.append(ins(f"v_mov_b32_e32 {m1}, {m0}", "valu", dst=m1, src=m0))
-    L.append(ins(f"v_permlane32_swap_b32_e32 {m0}, {m1}", "perm", dst=f"{m0} {m1}", src=f"{m0} {m1}"))
-    for qg in range(2):
-        m = v(MX + qg)
-        L.append(ins(f"v_mul_f32_e32 {m}, %[c2], {m}", "valu", dst=m, src=m))
-    for qg in range(2):
-        L.append(ins(f"v_add_f32_e32 {v(MNEW + qg)}, {TAU}, {v(MREF + qg)}", "valu", dst=v(MNEW + qg),
-                     src=v(MREF + qg)))
-    for qg in range(2):
-        m = v(MX + qg)
-        L.append(ins(f"v_max_f32_e32 {v(MMAX + qg)}, {v(MMAX + qg)}, {m}", "valu", dst=v(MMAX + qg),
-                     src=f"{v(MMAX + qg)} {m}"))
-        L.append(ins(f"v_cmp_gt_f32_e64 {s(F[qg], 2)}, {m}, {v(MNEW + qg)}", "valu", dst=s(F[qg], 2),
-                     src=f"{m} {v(MNEW + qg)}"))
-    for qg in range(2):
-        m = v(MX + qg)
-        L.append(ins(f"v_cndmask_b32_e64 {v(MNEW + qg)}, {v(MREF + qg)}, {m}, {s(F[qg], 2)}", "valu",
-                     dst=v(MNEW + qg), src=f"{v(MREF + qg)} {m} {s(F[qg], 2)}"))
-    L.append(ins(f"s_or_b64 {s(FLAG, 2)}, {s(F[0], 2)}, {s(F[1], 2)}", "salu", dst=s(FLAG, 2),
-                 src=f"{s(F[0], 2)} {s(F[1], 2)}"))
-    for qg in range(2):
-        L.append(ins(f"v_max_f32_e32 {v(MUSE + qg)}, {NEG_BIG}, {v(MNEW + qg)}", "valu", dst=v(MUSE + qg),
-                     src=v(MNEW + qg)))
-    order = [(qg, r) for r in range(16) for qg in range(2)]
-    fmas = {e: ins(f"v_fma_f32 {sv(*e)}, {sv(*e)}, %[c2], -{v(MUSE + e[0])}", "valu", dst=sv(*e),
-                   src=f"{sv(*e)} {v(MUSE + e[0])}") for e in order}
-    exps = {e: ins(f"v_exp_f32_e32 {sv(*e)}, {sv(*e)}", "trans", dst=sv(*e), src=sv(*e)) for e in order}
-    adds, cvts = {}, {}
-    for (qg, r) in order:
-        if r == 1:
-            adds[(qg, r)] = ins(f"v_add_f32_e32 {v(LSUM + qg)}, {sv(qg, 0)}, {sv(qg, 1)}", "valu", dst=v(LSUM + qg),
-                                src=f"{sv(qg, 0)} {sv(qg, 1)}")
-        elif r > 1:
-            adds[(qg, r)] = ins(f"v_add_f32_e32 {v(LSUM + qg)}, {v(LSUM + qg)}, {sv(qg, r)}", "valu",
-                                dst=v(LSUM + qg), src=f"{v(LSUM + qg)} {sv(qg, r)}")
-        if r % 2 == 1:
-            k2, j = r // 8, (r - 1) % 8
-            dst = v(pn + qg * 8 + k2 * 4 + j // 2)
-            cvts[(qg, r)] = ins(f"v_cvt_pk_bf16_f32 {dst}, {sv(qg, r - 1)}, {sv(qg, r)}", "valu", dst=dst,
-                                src=f"{sv(qg, r - 1)} {sv(qg, r)}")
-    n = len(order)
-    for k in range(n + SKEW_ADD + 2):  # skewed: fma(k), exp(k - SKEW_EXP), add / cvt(k - SKEW_ADD)
-        if k < n:
-            L.append(fmas[order[k]])
-        if 0 <= k - SKEW_EXP < n:
-            L.append(exps[order[k - SKEW_EXP]])
-        if 0 <= k - SKEW_ADD < n:
-            e = order[k - SKEW_ADD]
-            if e in adds:
-                L.append(adds[e])
-            if e in cvts:
-                L.append(cvts[e])
+            m = v(MMAX + qg)
+            mx.append(ins(f"v_max3_f32 {m}, {m}, {sv(qg, 2 * step)}, {sv(qg, 2 * step + 1)}", "valu", dst=m,
+                          src=f"{m} {sv(qg, 2 * step)} {sv(qg, 2 * step + 1)}"))
+    for i, x in enumerate(mx):
+        body.insert(8 + 5 * i, x)
+    L += body
+    for qg in range(2):  # a block sum above 2^8 (or inf) flags the wave for the rescale; NaN does not
+        L.append(ins(f"v_cmp_lt_f32_e32 vcc, {LIMIT}, {v(LSUM + qg)}", "valu", dst=["vcc"], src=v(LSUM + qg)))
+        L.append(ins(f"s_or_b64 {s(FLAG, 2)}, {s(FLAG, 2)}, vcc", "salu", dst=s(FLAG, 2),
+                     src=[*regs_of(s(FLAG, 2)), "vcc"]))
     return L
 
 
@@ -313,6 +310,8 @@ def prologue(probe=False):
         em.raw(f"v_mov_b32 {v(r)}, 0", 1)
     for r in range(128):
         em.raw(f"v_accvgpr_write_b32 {a(r)}, 0", 1)
+    for qg in range(2):  # m_ref: the first keys of a row overflow their exps and so flag the rescale
+        em.raw(f"v_mov_b32 {v(MREF + qg)}, {NEG_BIG}", 1)
     em.raw("s_cmp_eq_u32 %[nb], 0")
     em.raw(f"s_cbranch_scc1 {lbl('done')}")
     em.raw("s_waitcnt lgkmcnt(0)")  # the zero fill of V buffer 7 (O(-1) reads it with P = 0)
@@ -341,21 +340,30 @@ def prologue(probe=False):
     return em
 
 
-def rescale():
-    """O and l to the new reference point m_new, per lane: corr = 2^(m_ref -
-    m_new) (1 where unchanged, including -inf == -inf)."""
+def rescale(par):
+    """After slot J (parity par) flagged: m_ref moves to c2 times the row's
+    running maximum over both lane halves (at least -FLT_MAX), O and l are
+    multiplied by corr = 2^(m_ref - m_new) (m_new >= m_ref: 1 where
+    unchanged, 0 from -FLT_MAX), and P(J) and the block sums are computed
+    again against the new reference from S(J)."""
     em = Emitter()
     em.nop(16)  # the last O MFMAs of the slot
+    m0, m1 = v(MX), v(MX + 1)
     for qg in range(2):
-        t = v(TMP + qg)
-        em.emit(ins(f"v_sub_f32_e32 {t}, {v(MREF + qg)}, {v(MNEW + qg)}", "valu", dst=t,
-                    src=f"{v(MREF + qg)} {v(MNEW + qg)}"))
-        em.emit(ins(f"v_exp_f32_e32 {t}, {t}", "trans", dst=t, src=t))
-        em.emit(ins(f"v_cmp_eq_f32_e64 {s(MK[qg], 2)}, {v(MREF + qg)}, {v(MNEW + qg)}", "valu", dst=s(MK[qg], 2),
-                    src=f"{v(MREF + qg)} {v(MNEW + qg)}"))
+        em.emit(ins(f"v_mov_b32_e32 {v(MX + qg)}, {v(MMAX + qg)}", "valu", dst=v(MX + qg), src=v(MMAX + qg)))
+    # [mx0 lo | mx0 hi], [mx1 lo | mx1 hi] -> swap, max -> [M0 | M1] -> copy, swap -> [M0 | M0], [M1 | M1]
+    em.emit(ins(f"v_permlane32_swap_b32_e32 {m0}, {m1}", "perm", dst=f"{m0} {m1}", src=f"{m0} {m1}"))
+    em.emit(ins(f"v_max_f32_e32 {m0}, {m0}, {m1}", "valu", dst=m0, src=f"{m0} {m1}"))
+    em.emit(ins(f"v_mov_b32_e32 {m1}, {m0}", "valu", dst=m1, src=m0))
+    em.emit(ins(f"v_permlane32_swap_b32_e32 {m0}, {m1}", "perm", dst=f"{m0} {m1}", src=f"{m0} {m1}"))
     for qg in range(2):
-        c, t = v(CORR + qg), v(TMP + qg)
-        em.emit(ins(f"v_cndmask_b32_e64 {c}, {t}, 1.0, {s(MK[qg], 2)}", "valu", dst=c, src=f"{t} {s(MK[qg], 2)}"))
+        mn, t, c = v(MNEW + qg), v(TMP + qg), v(CORR + qg)
+        em.emit(ins(f"v_mul_f32_e32 {mn}, %[c2], {v(MX + qg)}", "valu", dst=mn, src=v(MX + qg)))
+        em.emit(ins(f"v_max_f32_e32 {mn}, {NEG_BIG}, {mn}", "valu", dst=mn, src=mn))
+        em.emit(ins(f"v_sub_f32_e32 {t}, {v(MREF + qg)}, {mn}", "valu", dst=t, src=f"{v(MREF + qg)} {mn}"))
+        em.emit(ins(f"v_exp_f32_e32 {c}, {t}", "trans", dst=c, src=t))
+    for qg in range(2):
+        c = v(CORR + qg)
         em.emit(ins(f"v_mul_f32_e32 {v(LRUN + qg)}, {v(LRUN + qg)}, {c}", "valu", dst=v(LRUN + qg),
                     src=f"{v(LRUN + qg)} {c}"))
         em.emit(ins(f"v_mov_b32_e32 {v(MREF + qg)}, {v(MNEW + qg)}", "valu", dst=v(MREF + qg), src=v(MNEW + qg)))
@@ -370,6 +378,7 @@ def rescale():
         for k in range(8):
             t = v(TMP + k)
             em.emit(ins(f"v_accvgpr_write_b32 {a(base + k)}, {t}", "valu", dst=a(base + k), src=t))
+    em.emit_all(exp_pipeline(par))
     em.nop(4)
     return em
 
@@ -397,7 +406,7 @@ def build(probe=False):
     """The loop's lines; probe: the bench-only variant whose copy cursor wraps
     around one source buffer instead of walking the chunk table."""
     pro = prologue(probe)
-    resc = rescale()
+    resc = (rescale(0), rescale(1))
     # fixed point of the slot boundary states: slot u is entered from slot
     # u - 1 (plain, masked or through the rescale), slot 0 also from the
     # prologue
@@ -409,7 +418,7 @@ def build(probe=False):
             prev = ends[(u - 1) % 8] + ([pro] if u == 0 else [])
             new[u] = (slot_body(u, prev or [pro], False), slot_body(u, prev or [pro], True))
         bodies = new
-        ends = {u: [bodies[u][0], bodies[u][1], resc] for u in range(8)}
+        ends = {u: [bodies[u][0], bodies[u][1], resc[u % 2]] for u in range(8)}
     lines = []
     lines += pro.lines
     lines.append(f"{lbl('loop')}:")
@@ -438,16 +447,17 @@ def build(probe=False):
     for u in range(8):
         lines.append(f"{lbl(f'resc{u}')}:")
         lines.append(f"s_mov_b32 {s(U)}, {u}")
-        lines.append(f"s_branch {lbl('rescale')}")
-    lines.append(f"{lbl('rescale')}:")
-    lines += resc.lines
-    lines.append(f"s_mov_b64 {s(FLAG, 2)}, 0")
-    for u in range(8):
-        lines.append(f"s_cmp_eq_u32 {s(U)}, {u}")
-        lines.append(f"s_cbranch_scc1 {lbl(f'ret{u}')}")
+        lines.append(f"s_branch {lbl(f'rescale{u % 2}')}")
+    for par in range(2):
+        lines.append(f"{lbl(f'rescale{par}')}:")
+        lines += resc[par].lines
+        lines.append(f"s_mov_b64 {s(FLAG, 2)}, 0")
+        for u in range(par, 8, 2):
+            lines.append(f"s_cmp_eq_u32 {s(U)}, {u}")
+            lines.append(f"s_cbranch_scc1 {lbl(f'ret{u}')}")
     for u in range(8):
         lines.append(f"{lbl(f'exit{u}')}:")
-        lines += final_o(u, [bodies[u][0], bodies[u][1], resc]).lines
+        lines += final_o(u, [bodies[u][0], bodies[u][1], *resc]).lines
         lines.append(f"s_branch {lbl('done')}")
     lines.append(f"{lbl('done')}:")
     lines.append("s_waitcnt vmcnt(0) lgkmcnt(0)")

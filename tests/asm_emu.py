@@ -139,6 +139,8 @@ class Emu:
             return wv.s.get(i, 0) | (wv.s.get(i + 1, 0) << 32)
         if tok == 'm0':
             return wv.m0
+        if tok == 'vcc':
+            return sum(1 << l for l in range(64) if wv.vcc[l])
         return int(tok, 0)
 
     def vsrc(self, wv, tok):
@@ -384,7 +386,8 @@ class Emu:
             x = (self.fsrc(wv, args[1]).astype(np.float64) * self.fsrc(wv, args[2]) + self.fsrc(wv, args[3]))
             wv.v[reg(args[0])[1]] = x.astype(np.float32).view(np.uint32)
         elif op == 'v_exp_f32_e32':
-            x = np.exp2(self.fsrc(wv, args[1]).astype(np.float64))
+            with np.errstate(over='ignore'):  # exps that overflow to inf, as the hardware's do
+                x = np.exp2(self.fsrc(wv, args[1]).astype(np.float64))
             wv.v[reg(args[0])[1]] = x.astype(np.float32).view(np.uint32)
         elif op in ('v_add_f32_e32', 'v_sub_f32_e32', 'v_max_f32_e32'):
             a_, b_ = self.fsrc(wv, args[1]), self.fsrc(wv, args[2])
@@ -396,9 +399,10 @@ class Emu:
         elif op == 'v_sub_u32_e32':
             wv.v[reg(args[0])[1]] = (self.vsrc(wv, args[1]).astype(np.int64) -
                                      self.vsrc(wv, args[2]).astype(np.int64)).astype(np.uint32)
-        elif op in ('v_cmp_gt_f32_e64', 'v_cmp_eq_f32_e64'):
+        elif op in ('v_cmp_gt_f32_e64', 'v_cmp_eq_f32_e64', 'v_cmp_lt_f32_e32'):
             a_, b_ = self.fsrc(wv, args[1]), self.fsrc(wv, args[2])
-            self.set_mask(wv, args[0], a_ > b_ if op == 'v_cmp_gt_f32_e64' else a_ == b_)
+            m = {'v_cmp_gt_f32_e64': a_ > b_, 'v_cmp_eq_f32_e64': a_ == b_, 'v_cmp_lt_f32_e32': a_ < b_}[op]
+            self.set_mask(wv, args[0], m)
         elif op == 'v_cmp_ge_i32_e32':
             a_ = self.vsrc(wv, args[1]).view(np.int32)
             b_ = self.vsrc(wv, args[2]).view(np.int32)
@@ -735,7 +739,8 @@ def run_fwd_block(q, ks, vs, lens, order, scale, lines=None):
         vf = waves[w].v.view(np.float32)
         af = waves[w].a.view(np.float32)
         for qg in range(2):
-            m_ref, m_max, l = vf[50 + qg], vf[52 + qg], vf[54 + qg]
+            m_ref, l = vf[50 + qg], vf[54 + qg]
+            m_max = c2 * np.maximum(vf[52 + qg], np.roll(vf[52 + qg], 32))  # lanes' running raw maxima
             l_tot = l + np.roll(l, 32)
             for ln in range(64):
                 qi = w * 64 + qg * 32 + (ln & 31)
