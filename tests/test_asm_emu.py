@@ -6,7 +6,8 @@ instruction-level model in tests/asm_emu.py, against fp64
   dQ and forward (dq_asm_gen.py, fwd_asm_gen.py): every loop exit with and
     without a partial last block, the copy cursor through tiny and empty
     chunks in ring order, the forward's lazy rescale;
-and planted mistakes (a layout swap, a dropped cursor advance) shown to fail."""
+and planted mistakes (a layout swap, a dropped cursor advance, a rescale
+that does not compute the flagged block again) shown to fail."""
 
 import numpy as np
 import pytest
@@ -153,3 +154,28 @@ def test_planted_cursor_error_is_caught():
     dq = emu.run_dq_block(q, do, ks, vs, lens, [0], (-lse / scale).astype(np.float32), (-D).astype(np.float32),
                           scale, lines=bad)
     assert _rel(dq, dqr) > 0.05
+
+
+@pytest.mark.filterwarnings("ignore:invalid value encountered in matmul")  # the stale inf P
+def test_planted_missing_recompute_in_the_rescale_is_caught():
+    """The forward's rescale must compute the flagged block's P again against
+    the new reference point (the first block's exps overflow against the
+    starting -FLT_MAX): dropping the packs of that recompute must fail."""
+    lens = [96, 96]
+    q, do, ks, vs = _qkv(40, lens, 96, seed=4)
+    scale = 1 / np.sqrt(128)
+    O, lse_r, m_r, *_ = emu.attention_reference(q, ks, vs, lens, scale)
+    lines = emu.GF.build()
+    bad, in_resc = [], False
+    for ln in lines:
+        if ln.startswith(".Lfa_rescale"):
+            in_resc = True
+        elif ln.startswith("s_mov_b64 s[64:65], 0"):
+            in_resc = False
+        if in_resc and ln.startswith("v_cvt_pk_bf16_f32"):
+            continue
+        bad.append(ln)
+    assert len(bad) < len(lines)
+    Of, mf, lf = emu.run_fwd_block(q, ks, vs, lens, [0, 1], scale, lines=bad)
+    err = _rel(Of, O)
+    assert not np.isfinite(err) or err > 0.05
