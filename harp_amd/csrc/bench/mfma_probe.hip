@@ -481,7 +481,7 @@ __global__ __launch_bounds__(256, 1) void dkdv_asm_probe_kernel(uint32_t seed, i
       for (int db = 0; db < 4; ++db) {
         const int row = 8 * hh + 4 * g + sr;
         mv[8 + hh * 4 + db] =
-            (int)(lds0 + 4 * kDkBuf + 2 * (row * 128 + (((4 * db + cl) ^ fa_swz(row)) << 3) + 4 * (m & 1)));
+            (int)(lds0 + kDkBuf + 2 * (row * 128 + (((4 * db + cl) ^ fa_swz(row)) << 3) + 4 * (m & 1)));
       }
     mv[16] = (int)(lds0 + kDkVOff + (wave * 64 + l32) * kDkVRow + g * 16);
     mv[17] = (int)(lds0 + kDkStats + wave * kDkStatsPerWave + g * 16);

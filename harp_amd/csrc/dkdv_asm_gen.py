@@ -27,8 +27,9 @@ Slot J (one per query block):
          MFMAs that read the previous block's have issued; P = exp2(S c) of
          block J + 1 after its S MFMAs (clamped to [0, 1])
   copies of block J + 3 (Q, dO rows and the statistics rows)
-The read address registers are moved to the next slot's buffers at fixed
-points (ds_read offsets reach 64 KiB, the five buffers span 80 KiB).
+The read address registers point at a base buffer and the offsets select the
+buffer (ds_read offsets reach 64 KiB: four of the five buffers from a base);
+they move between base buffers 0 and 1 twice per trip around the buffers.
 Query rows past T load as zero with zero statistics: their P is 1 but their
 dO and Q rows are zero, so they add nothing.  Pad keys (past the chunk's
 valid length) get zero dK / dV in the kernel's epilogue.
@@ -97,13 +98,14 @@ def p1_pair(n):
     return out
 
 
-def t_read(n):
+def t_read(n, rel):
     """transposed fragment of pair n: dO^T (even n) or Q^T (odd n), queries
-    16 h2 .., d block db, from the buffer TADDR points at"""
+    16 h2 .., d block db, from the buffer rel above the one TADDR points at"""
     idx = n // 2
     h2, db = idx // 4, idx % 4
     f = T_RING[n % 4]
-    off = (GOFF if n % 2 == 0 else QOFF) + h2 * 4096
+    off = rel * BUF + (GOFF if n % 2 == 0 else QOFF) + h2 * 4096
+    assert 0 <= off < 65536
     return [ins(f"ds_read_b64_tr_b16 {v(f, 2)}, {v(TADDR + db)} offset:{off}", "ds", dst=v(f, 2), src=v(TADDR + db)),
             ins(f"ds_read_b64_tr_b16 {v(f + 2, 2)}, {v(TADDR + 4 + db)} offset:{off}", "ds", dst=v(f + 2, 2),
                 src=v(TADDR + 4 + db))]
@@ -126,10 +128,12 @@ def p2_pair(m):
     return out
 
 
-def a_read(m):
+def a_read(m, rel):
+    """row fragment of phase-2 pair m from the buffer rel above the one RADDR points at"""
     ks = m % 8
     f = A_RING[m % 3]
-    off = (QOFF if m < 8 else GOFF)
+    off = rel * BUF + (QOFF if m < 8 else GOFF)
+    assert 0 <= off < 65536
     return [ins(f"ds_read_b128 {v(f, 4)}, {v(RADDR + ks)} offset:{off}", "ds", dst=v(f, 4), src=v(RADDR + ks))]
 
 
@@ -235,9 +239,24 @@ DMA_AT = (1, 7, 13, 19, 25, 29)
 SPLIT = 32       # the next block's first SPLIT exp-chain instructions run in this slot, the rest in the next
 
 
+def r_base(u):
+    """base buffer of RADDR in slot u, which reads block J + 1's rows (buffer u + 1)"""
+    return 0 if (u + 1) % NBUF == 0 else 1
+
+
+def t_base(u):
+    """base buffer of TADDR in slot u's phase 1, which reads block J - 1's (buffer u - 1)"""
+    return 0 if (u - 1) % NBUF < NBUF - 1 else 1
+
+
+TADDR_BUF0 = t_base(0)  # where the kernel points TADDR (slot 0 reads buffer NBUF - 1: block -1, zeros)
+
+
 def slot_body(u, entry):
-    """slot J (J % 5 == u): RADDR at block J + 1's buffer, TADDR at block J - 1's"""
+    """slot J (J % 5 == u): RADDR reads block J + 1's buffer, TADDR block J - 1's"""
     rbuf, dmabuf = (u + 1) % NBUF, (u + AHEAD) % NBUF
+    trel, rrel = (u - 1) % NBUF - t_base(u), rbuf - r_base(u)
+    nt = (u + 1) % NBUF  # the next slot
     em = Emitter.merged_entry(entry)
     mf_list = []
     for n in range(16):
@@ -249,26 +268,27 @@ def slot_body(u, entry):
     def pin(k, lst):
         pinned.setdefault(k, []).extend(lst)
     for n in range(2, 16):
-        pin(2 * (n - 2), t_read(n))
+        pin(2 * (n - 2), t_read(n, trel))
     pin(2, init_reads(rbuf))
     for i, at in enumerate(DMA_AT):
         pin(at, dma(i, dmabuf))
-    pin(28, a_read(0))
-    pin(30, a_read(1))
+    pin(28, a_read(0, rrel))
+    pin(30, a_read(1, rrel))
     for m in range(2, 16):
-        pin(P2 + 2 * (m - 2), a_read(m))
+        pin(P2 + 2 * (m - 2), a_read(m, rrel))
     pin(P2 + 8, v_reads(0))
     pin(P2 + 12, v_reads(1))
     for ks in range(2, 8):
         pin(P2 + 2 * (8 + ks - 1), v_reads(ks))
-    # TADDR to the next slot's dV / dK buffer (block J), then its first two fragments
-    nb_t = u                       # block J's buffer
-    cur_t = (u + NBUF - 1) % NBUF  # block J - 1's
-    pin(P2, rebase(TADDR, (nb_t - cur_t) * BUF))
-    pin(P2 + 18, t_read(0))
-    pin(P2 + 22, t_read(1))
-    # RADDR to the next slot's S / dP buffer (block J + 2) after the last row read
-    pin(P2 + 30, rebase(RADDR, (((u + 2) % NBUF) - rbuf) * BUF))
+    # TADDR to the next slot's base (when it changes), then the next slot's
+    # first two fragments (block J, buffer u)
+    if t_base(nt) != t_base(u):
+        pin(P2, rebase(TADDR, (t_base(nt) - t_base(u)) * BUF))
+    pin(P2 + 18, t_read(0, u - t_base(nt)))
+    pin(P2 + 22, t_read(1, u - t_base(nt)))
+    # RADDR to the next slot's base after the last row read
+    if r_base(nt) != r_base(u):
+        pin(P2 + 30, rebase(RADDR, (r_base(nt) - r_base(u)) * BUF))
     fillers = s_part(0)[SPLIT:] + dp_part() + s_part(P2 + 16)[:SPLIT]
     left = fill_schedule(em, mf_list, fillers, budget=BUDGET, pinned=pinned, flush_war=True)
     em.emit_all(left)
@@ -299,30 +319,30 @@ def prologue(probe=False):
     mfl = []
     for m in range(16):
         mfl += p2_pair(m)
-    pinned = {0: a_read(0) + a_read(1) + v_reads(0) + v_reads(1)}
+    pinned = {0: a_read(0, 0) + a_read(1, 0) + v_reads(0) + v_reads(1)}
     for m in range(2, 16):
-        pinned.setdefault(2 * (m - 2), []).extend(a_read(m))
+        pinned.setdefault(2 * (m - 2), []).extend(a_read(m, 0))
     for ks in range(2, 8):
         pinned.setdefault(2 * (8 + ks - 1), []).extend(v_reads(ks))
     left = fill_schedule(em, mfl, s_part(16)[:SPLIT], budget=BUDGET, pinned=pinned)
     em.emit_all(left)
-    # slot 0 reads S / dP rows from buffer 1; its dV / dK fragments (block -1,
-    # zeros) from buffer 4, where TADDR starts
-    em.emit_all(rebase(RADDR, BUF))
-    em.emit_all(t_read(0) + t_read(1))
+    # slot 0 reads S / dP rows from buffer 1 (RADDR to its base); its dV / dK
+    # fragments (block -1, zeros) from buffer NBUF - 1
+    em.emit_all(rebase(RADDR, r_base(0) * BUF))
+    em.emit_all(t_read(0, NBUF - 1 - TADDR_BUF0) + t_read(1, NBUF - 1 - TADDR_BUF0))
     return em
 
 
-def final_dvdk(entry):
-    """dV / dK of the last block after its slot: P / dS packed there, TADDR
-    at its buffer, the first two fragments read"""
+def final_dvdk(u, entry):
+    """dV / dK of the last block after its slot u: P / dS packed there, TADDR
+    at the next slot's base, the first two fragments read"""
     em = Emitter.merged_entry(entry)
     mfl = []
     for n in range(16):
         mfl += p1_pair(n)
     pinned = {}
     for n in range(2, 16):
-        pinned.setdefault(2 * (n - 2), []).extend(t_read(n))
+        pinned.setdefault(2 * (n - 2), []).extend(t_read(n, u - t_base((u + 1) % NBUF)))
     fill_schedule(em, mfl, [], pinned=pinned)
     em.settle()
     return em
@@ -350,10 +370,12 @@ def build(probe=False):
         lines += desc_advance(probe)
         lines.append(f"s_add_u32 {s(J)}, {s(J)}, 1")
         lines.append(f"s_cmp_eq_u32 {s(J)}, %[nb]")
-        lines.append(f"s_cbranch_scc1 {lbl('exit')}")
+        lines.append(f"s_cbranch_scc1 {lbl(f'exit{u}')}")
     lines.append(f"s_branch {lbl('loop')}")
-    lines.append(f"{lbl('exit')}:")
-    lines += final_dvdk([bodies[u] for u in range(NBUF)]).lines
+    for u in range(NBUF):
+        lines.append(f"{lbl(f'exit{u}')}:")
+        lines += final_dvdk(u, [bodies[u]]).lines
+        lines.append(f"s_branch {lbl('done')}")
     lines.append(f"{lbl('done')}:")
     lines.append("s_waitcnt vmcnt(0) lgkmcnt(0)")
     return lines

@@ -475,8 +475,8 @@ def run_block(q, k, v, do, stats0, stats1, scale, len_valid, kblk0=0):
         for hh in range(2):
             for db in range(4):
                 row = 8 * hh + 4 * g + sr
-                mv[8 + hh * 4 + db] = 4 * KBUF + 2 * (row * 128 + (((4 * db + cl) ^ np.vectorize(swz)(row)) << 3)
-                                                      + 4 * (m & 1))
+                mv[8 + hh * 4 + db] = G.TADDR_BUF0 * KBUF + 2 * (row * 128 + (((4 * db + cl) ^ np.vectorize(swz)(row))
+                                                                 << 3) + 4 * (m & 1))
         mv[16] = KV_OFF + (w * 64 + l32) * VROW + g * 16
         mv[17] = ST_OFF + w * ST_PER_WAVE + g * 16
         for i in range(2):

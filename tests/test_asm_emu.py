@@ -1,8 +1,9 @@
 """CPU check of the generated hand-scheduled loops through the
 instruction-level model in tests/asm_emu.py, against fp64
 (ring_attn.cpp:2412-2575 forward, :2577-2829 backward):
-  dK/dV (dkdv_asm_gen.py): one 256-key block, query block counts over two
-    trips around the five LDS buffers, a ragged last query block, pad keys;
+  dK/dV (dkdv_asm_gen.py): one 256-key block, query block counts that leave
+    the loop from each of its five slots and over two trips around the LDS
+    buffers, a ragged last query block, pad keys;
   dQ and forward (dq_asm_gen.py, fwd_asm_gen.py): every loop exit with and
     without a partial last block, the copy cursor through tiny and empty
     chunks in ring order, the forward's lazy rescale;
@@ -29,7 +30,7 @@ def _case(T, len_valid, seed):
     return dk, dv, dkr, dvr
 
 
-@pytest.mark.parametrize("T", [32, 96, 160, 330])
+@pytest.mark.parametrize("T", [32, 64, 96, 128, 160, 330])  # leaves from every slot (nb - 1) % 5
 def test_loop_matches_fp64(T):
     dk, dv, dkr, dvr = _case(T, 256, seed=T)
     for name, a, b in (("dk", dk, dkr), ("dv", dv, dvr)):
