@@ -36,12 +36,9 @@ def run_hip(
     do_layout: str = "token",
     grad_dtype: torch.dtype = torch.bfloat16,
     backward: bool = True,
-    dkv_misalign: bool = False,
 ) -> Dict[str, torch.Tensor]:
     """Run forward (+ delta + backward) on the GPU; return CPU tensors:
-    o (fp32), lse (fp64), m, l, delta, dq, dk, dv (dk/dv concatenated over chunks).
-    dkv_misalign (C ABI only): dK / dV chunk views at an odd element offset
-    with an odd row stride, so their rows are only 2-byte aligned."""
+    o (fp32), lse (fp64), m, l, delta, dq, dk, dv (dk/dv concatenated over chunks)."""
     dev = torch.device("cuda")
     B, H, T, D = q.shape
     n = len(ks)
@@ -74,18 +71,15 @@ def run_hip(
             delta = torch.empty((B, H, T, 1), device=dev, dtype=torch.float32)
             hops.abi_delta(dod, out, delta)
             dq = torch.full((B, T, H, D), float("nan"), device=dev, dtype=grad_dtype).transpose(1, 2)
-            def grad_chunk():
-                if dkv_misalign:
-                    return torch.full((B, tc, H, D + 1), float("nan"), device=dev, dtype=grad_dtype)[..., 1:].transpose(1, 2)
-                return torch.full((B, tc, H, D), float("nan"), device=dev, dtype=grad_dtype).transpose(1, 2)
-            dk = [grad_chunk() for _ in range(n)]
-            dv = [grad_chunk() for _ in range(n)]
+            dk = [torch.full((B, tc, H, D), float("nan"), device=dev, dtype=grad_dtype).transpose(1, 2)
+                  for _ in range(n)]
+            dv = [torch.full((B, tc, H, D), float("nan"), device=dev, dtype=grad_dtype).transpose(1, 2)
+                  for _ in range(n)]
             hops.abi_backward(qd, dq, kd, vd, dk, dv, dod, m_i, l_i, delta, scale, ring_rank=ring_rank,
                               kv_lens=kv_lens)
             dk_all = torch.cat(dk, dim=2)
             dv_all = torch.cat(dv, dim=2)
         else:
-            assert not dkv_misalign, "dkv_misalign goes through the C ABI"
             delta = torch.ops.ring_attention_ops.ring_attention_delta(dod, out)
             dq = torch.full((B, T, H, D), float("nan"), device=dev, dtype=grad_dtype).transpose(1, 2)
             dk_all = torch.full((B, n * tc, H, D), float("nan"), device=dev, dtype=grad_dtype).transpose(1, 2)

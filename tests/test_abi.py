@@ -171,6 +171,9 @@ def _bwd_call(**over):
         (dict(ks=_lib.i64_array([0, 0, 0, 1])), "k chunk row stride"),
         (dict(dqs=_lib.i64_array([8 * 64 * 128, 64, 0, 1])), "grad_q strides make elements overlap"),
         (dict(dks=_lib.i64_array([8 * 64 * 128, 0, 8 * 64, 1])), "dK chunk strides make elements overlap"),
+        # bf16 dK / dV rows are stored 8 bytes per lane
+        (dict(dks=_lib.i64_array([8 * 66 * 128, 66, 8 * 66 + 2, 1])), "must be a multiple of 4 elements"),
+        (dict(dkc=_lib.ptr_array([(1 << 20) + 2])), "must be 8-byte aligned"),
     ],
 )
 def test_backward_rejects_degenerate_strides(over, msg):
