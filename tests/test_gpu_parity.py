@@ -369,10 +369,11 @@ def test_config2_robustness_seeds(seed):
 
 # --- randomized shapes ------------------------------------------------------------
 
-def _random_cases(n=16, seed=2024):
-    """Deterministic random problems: batch, heads, query rows, head dim,
-    chunk count and length, valid length per chunk (some chunks ragged or
-    empty, at least one key overall), ring rank, value scale."""
+def _random_cases(n=16, seed=2024, head_dim=None, max_rows=300, max_chunk=260):
+    """Deterministic random problems: batch, heads, query rows, head dim
+    (or head_dim), chunk count and length, valid length per chunk (some
+    chunks ragged or empty, at least one key overall), ring rank, value
+    scale."""
     g = torch.Generator().manual_seed(seed)
 
     def ri(lo, hi):
@@ -380,10 +381,10 @@ def _random_cases(n=16, seed=2024):
 
     cases = []
     for i in range(n):
-        B, H, T = ri(1, 2), ri(1, 4), ri(1, 300)
-        D = 8 * ri(1, 16)
+        B, H, T = ri(1, 2), ri(1, 4), ri(1, max_rows)
+        D = head_dim or 8 * ri(1, 16)
         N = ri(1, 5)
-        tc = ri(1, 260)
+        tc = ri(1, max_chunk)
         lens = [ri(0, tc) if ri(0, 2) else tc for _ in range(N)]
         if sum(lens) == 0:
             lens[0] = tc
@@ -403,3 +404,12 @@ def test_random_shapes(case):
     res = run_hip(q, ks, vs, do, scale, ring_rank=rank, kv_lens=lens, via="ops" if i % 2 else "abi")
     ref = _oracle_full(q, ks, vs, do, scale, rank=rank, lens=lens)
     _check_all(res, ref)
+
+
+@pytest.mark.parametrize("case", _random_cases(n=12, seed=4096, head_dim=128, max_rows=600, max_chunk=600),
+                         ids=lambda c: f"d128r{c[0]}")
+def test_random_shapes_head_dim_128(case):
+    """The same at D = 128 (the hand-scheduled loops), with up to 600 query
+    rows and 600-key chunks: many loop slots, every exit, ragged and empty
+    chunks in ring order."""
+    test_random_shapes(case)
