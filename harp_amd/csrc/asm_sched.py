@@ -34,6 +34,14 @@ def regs_of(s):
     return out
 
 
+def clobber_list(sgprs):
+    """The asm statement's clobber list for a loop that writes the SGPRs
+    `sgprs`: those, plus m0 (the LDS-DMA destination base) and scc (every
+    compare, 32-bit add and branch condition), so the compiler keeps no
+    value in either across the statement."""
+    return ", ".join([f'"s{r}"' for r in sgprs] + ['"m0"', '"scc"'])
+
+
 COST = {"mfma": 32, "valu": 4, "trans": 8, "perm": 8, "ds": 4, "vmem": 4, "salu": 1, "m0": 1}
 
 

@@ -41,7 +41,7 @@ import os
 import sys
 
 sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
-from asm_sched import Emitter, fill_schedule, ins  # noqa: E402
+from asm_sched import Emitter, clobber_list, fill_schedule, ins  # noqa: E402
 from fwd_asm_gen import a, lbl, s, v  # noqa: E402
 
 # ---- registers ------------------------------------------------------------
@@ -174,12 +174,9 @@ def dma(i, buf):
             ins(f"buffer_load_dword {v(SOFF)}, {desc}, 0 offen lds", "vmem", src=[v(SOFF), "m0"])]
 
 
-def desc_advance(probe=False):
-    """the four descriptors to the next query block (bytes left clamped at 0);
-    probe: they stay on the one source block (the bench-only probe)"""
+def desc_advance():
+    """the four descriptors to the next query block (bytes left clamped at 0)"""
     out = []
-    if probe:
-        return out
     for d, step in ((DQ, "%[qstep]"), (DG, "%[gstep]"), (DS0, "128"), (DS1, "128")):
         out += [f"s_add_u32 {s(d)}, {s(d)}, {step}",
                 f"s_addc_u32 {s(d + 1)}, {s(d + 1)}, 0",
@@ -295,7 +292,7 @@ def slot_body(u, entry):
     return em
 
 
-def prologue(probe=False):
+def prologue():
     em = Emitter()
     for r in range(PB, DSB + 16):  # P, dS of block -1: zero
         em.raw(f"v_mov_b32 {v(r)}, 0", 1)
@@ -311,7 +308,7 @@ def prologue(probe=False):
     for blk in range(AHEAD):
         for i in range(6):
             em.emit_all(dma(i, blk))
-        for line in desc_advance(probe):
+        for line in desc_advance():
             em.raw(line, 1)
     em.raw(f"s_waitcnt vmcnt({6 * (AHEAD - 1)})")  # block 0 (this wave's part)
     em.raw("s_barrier")
@@ -348,10 +345,9 @@ def final_dvdk(u, entry):
     return em
 
 
-def build(probe=False):
-    """The loop's lines; probe: the bench-only variant whose copies re-read
-    one query block instead of walking the query rows."""
-    pro = prologue(probe)
+def build():
+    """The loop's lines."""
+    pro = prologue()
     bodies, ends = {}, {u: [] for u in range(NBUF)}
     for _ in range(4):
         new = {}
@@ -367,7 +363,7 @@ def build(probe=False):
         # statistics) must have landed for every wave
         lines += [f"s_waitcnt vmcnt({6 * (AHEAD - 2)})", "s_barrier"]
         lines += bodies[u].lines
-        lines += desc_advance(probe)
+        lines += desc_advance()
         lines.append(f"s_add_u32 {s(J)}, {s(J)}, 1")
         lines.append(f"s_cmp_eq_u32 {s(J)}, %[nb]")
         lines.append(f"s_cbranch_scc1 {lbl(f'exit{u}')}")
@@ -381,21 +377,19 @@ def build(probe=False):
     return lines
 
 
-def render(lines, probe_lines):
+def render(lines):
     def body(ls):
         return " \\\n".join('  "' + ln + '\\n\\t"' for ln in ls)
-    return ("// Generated by dkdv_asm_gen.py: the main loop of dkdv_asm_kernel (dkdv_asm.hip),\n"
-            "// and the same loop over one query block for the bench-only probe\n"
-            "// (bench/mfma_probe.hip).  Do not edit; change the generator and rebuild.\n"
+    return ("// Generated by dkdv_asm_gen.py: the main loop of dkdv_asm_kernel (dkdv_asm.hip).\n"
+            "// Do not edit; change the generator and rebuild.\n"
             "#pragma once\n"
-            f"#define HARP_DKDV_ASM_SGPR_CLOBBERS {', '.join(chr(34) + f's{r}' + chr(34) for r in SGPR_CLOBBER)}\n"
-            f"#define HARP_DKDV_ASM_LOOP \\\n{body(lines)}\n"
-            f"#define HARP_DKDV_ASM_PROBE \\\n{body(probe_lines)}\n")
+            f"#define HARP_DKDV_ASM_SGPR_CLOBBERS {clobber_list(SGPR_CLOBBER)}\n"
+            f"#define HARP_DKDV_ASM_LOOP \\\n{body(lines)}\n")
 
 
 def write(path=None):
     path = path or os.path.join(os.path.dirname(os.path.abspath(__file__)), "dkdv_asm.inc")
-    text = render(build(), build(probe=True))
+    text = render(build())
     old = open(path).read() if os.path.exists(path) else None
     if old != text:
         with open(path, "w") as f:

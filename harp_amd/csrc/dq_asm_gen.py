@@ -28,7 +28,7 @@ import os
 import sys
 
 sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
-from asm_sched import Emitter, fill_schedule, ins  # noqa: E402
+from asm_sched import Emitter, clobber_list, fill_schedule, ins  # noqa: E402
 from fwd_asm_gen import (DK, DV, FLAG, J, LEFT, RING, SGPR_CLOBBER, STEP, a, cursor_adv, cursor_desc,  # noqa: E402
                          lbl, s, v)
 
@@ -165,7 +165,7 @@ def slot_body(u, entry):
     return em
 
 
-def prologue(probe=False):
+def prologue():
     em = Emitter()
     for r in range(KF, DS + 16):  # fragments and dS(-1) = 0
         em.raw(f"v_mov_b32 {v(r)}, 0", 1)
@@ -184,7 +184,7 @@ def prologue(probe=False):
             em.raw(line, 1)
         for i in range(4):
             em.emit_all(dma(i, b))
-        for line in cursor_adv(f"p{b}", probe):
+        for line in cursor_adv(f"p{b}"):
             em.raw(line, 1)
     em.raw("s_waitcnt vmcnt(16)")  # block 0 (this wave's part)
     em.raw("s_barrier")
@@ -214,10 +214,9 @@ def final_dq(u, entry):
     return em
 
 
-def build(probe=False):
-    """The loop's lines; probe: the bench-only variant whose copy cursor wraps
-    around one source buffer instead of walking the chunk table."""
-    pro = prologue(probe)
+def build():
+    """The loop's lines."""
+    pro = prologue()
     bodies, ends = {}, {u: [] for u in range(8)}
     for _ in range(4):
         new = {}
@@ -233,7 +232,7 @@ def build(probe=False):
             lines += ["s_waitcnt vmcnt(8)", "s_barrier"]
         lines += cursor_desc((u + 5) % 8)
         lines += bodies[u].lines
-        lines += cursor_adv(f"s{u}", probe)
+        lines += cursor_adv(f"s{u}")
         lines.append(f"s_add_u32 {s(J)}, {s(J)}, 1")
         lines.append(f"s_cmp_eq_u32 {s(J)}, %[nb]")
         lines.append(f"s_cbranch_scc1 {lbl(f'exit{u}')}")
@@ -247,21 +246,19 @@ def build(probe=False):
     return lines
 
 
-def render(lines, probe_lines):
+def render(lines):
     def body(ls):
         return " \\\n".join('  "' + ln + '\\n\\t"' for ln in ls)
-    return ("// Generated by dq_asm_gen.py: the main loop of dq_asm_kernel (dq_asm.hip),\n"
-            "// and the same loop over one source buffer for the bench-only probe\n"
-            "// (bench/mfma_probe.hip).  Do not edit; change the generator and rebuild.\n"
+    return ("// Generated by dq_asm_gen.py: the main loop of dq_asm_kernel (dq_asm.hip).\n"
+            "// Do not edit; change the generator and rebuild.\n"
             "#pragma once\n"
-            f"#define HARP_DQ_ASM_SGPR_CLOBBERS {', '.join(chr(34) + f's{r}' + chr(34) for r in SGPR_CLOBBER)}\n"
-            f"#define HARP_DQ_ASM_LOOP \\\n{body(lines)}\n"
-            f"#define HARP_DQ_ASM_PROBE \\\n{body(probe_lines)}\n")
+            f"#define HARP_DQ_ASM_SGPR_CLOBBERS {clobber_list(SGPR_CLOBBER)}\n"
+            f"#define HARP_DQ_ASM_LOOP \\\n{body(lines)}\n")
 
 
 def write(path=None):
     path = path or os.path.join(os.path.dirname(os.path.abspath(__file__)), "dq_asm.inc")
-    text = render(build(), build(probe=True))
+    text = render(build())
     old = open(path).read() if os.path.exists(path) else None
     if old != text:
         with open(path, "w") as f:

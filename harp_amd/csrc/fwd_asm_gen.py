@@ -37,7 +37,7 @@ import os
 import sys
 
 sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
-from asm_sched import Emitter, fill_schedule, ins, regs_of  # noqa: E402
+from asm_sched import Emitter, clobber_list, fill_schedule, ins, regs_of  # noqa: E402
 
 # ---- registers ------------------------------------------------------------
 KADDR, VADDR, DOFF = 32, 40, 48          # per-lane LDS addresses / copy offsets
@@ -246,25 +246,10 @@ def cursor_desc(block_ring_slot):
     ]
 
 
-def cursor_adv(tag, probe=False):
+def cursor_adv(tag):
     """Move the cursor 32 keys on (after the block's copies are issued): into
     the next non-empty chunk of the split when this one ends.  Row pointers
-    stay below 2^48, so words 1 of DK / DV keep a zero stride field.  probe:
-    back to the start of the one source instead (the bench-only probe)."""
-    if probe:
-        return [
-            f"s_add_u32 {s(DK)}, {s(DK)}, %[blkb]",
-            f"s_addc_u32 {s(DK + 1)}, {s(DK + 1)}, 0",
-            f"s_add_u32 {s(DV)}, {s(DV)}, %[blkb]",
-            f"s_addc_u32 {s(DV + 1)}, {s(DV + 1)}, 0",
-            f"s_sub_i32 {s(LEFT)}, {s(LEFT)}, 32",
-            f"s_cmp_gt_i32 {s(LEFT)}, 0",
-            f"s_cbranch_scc1 {lbl('cok' + tag)}",
-            f"s_mov_b64 {s(DK, 2)}, %[kp0]",
-            f"s_mov_b64 {s(DV, 2)}, %[vp0]",
-            f"s_mov_b32 {s(LEFT)}, %[left0]",
-            f"{lbl('cok' + tag)}:",
-        ]
+    stay below 2^48, so words 1 of DK / DV keep a zero stride field."""
     return [
         f"s_add_u32 {s(DK)}, {s(DK)}, %[blkb]",
         f"s_addc_u32 {s(DK + 1)}, {s(DK + 1)}, 0",
@@ -303,7 +288,7 @@ def cursor_adv(tag, probe=False):
     ]
 
 
-def prologue(probe=False):
+def prologue():
     em = Emitter()
     # fragments, P (P(-1) = 0) and O start at zero; a split without keys ends here
     for r in range(KF, P[1] + 16):
@@ -325,7 +310,7 @@ def prologue(probe=False):
             em.raw(line, 1)
         for i in range(4):
             em.emit_all(dma(i, b))
-        for line in cursor_adv(f"p{b}", probe):
+        for line in cursor_adv(f"p{b}"):
             em.raw(line, 1)
     em.raw("s_waitcnt vmcnt(16)")  # block 0 (this wave's part)
     em.raw("s_barrier")
@@ -402,10 +387,9 @@ def final_o(u, entry):
     return em
 
 
-def build(probe=False):
-    """The loop's lines; probe: the bench-only variant whose copy cursor wraps
-    around one source buffer instead of walking the chunk table."""
-    pro = prologue(probe)
+def build():
+    """The loop's lines."""
+    pro = prologue()
     resc = (rescale(0), rescale(1))
     # fixed point of the slot boundary states: slot u is entered from slot
     # u - 1 (plain, masked or through the rescale), slot 0 also from the
@@ -431,7 +415,7 @@ def build(probe=False):
         lines.append(f"s_cbranch_scc1 {lbl(f'mask{u}')}")
         lines += bodies[u][0].lines
         lines.append(f"{lbl(f'join{u}')}:")
-        lines += cursor_adv(f"s{u}", probe)
+        lines += cursor_adv(f"s{u}")
         lines.append(f"s_cmp_lg_u64 {s(FLAG, 2)}, 0")
         lines.append(f"s_cbranch_scc1 {lbl(f'resc{u}')}")
         lines.append(f"{lbl(f'ret{u}')}:")
@@ -464,21 +448,19 @@ def build(probe=False):
     return lines
 
 
-def render(lines, probe_lines):
+def render(lines):
     def body(ls):
         return " \\\n".join('  "' + ln + '\\n\\t"' for ln in ls)
-    return ("// Generated by fwd_asm_gen.py: the main loop of fwd_asm_kernel (fwd_asm.hip),\n"
-            "// and the same loop over one source buffer for the bench-only probe\n"
-            "// (bench/mfma_probe.hip).  Do not edit; change the generator and rebuild.\n"
+    return ("// Generated by fwd_asm_gen.py: the main loop of fwd_asm_kernel (fwd_asm.hip).\n"
+            "// Do not edit; change the generator and rebuild.\n"
             "#pragma once\n"
-            f"#define HARP_FWD_ASM_SGPR_CLOBBERS {', '.join(chr(34) + f's{r}' + chr(34) for r in SGPR_CLOBBER)}\n"
-            f"#define HARP_FWD_ASM_LOOP \\\n{body(lines)}\n"
-            f"#define HARP_FWD_ASM_PROBE \\\n{body(probe_lines)}\n")
+            f"#define HARP_FWD_ASM_SGPR_CLOBBERS {clobber_list(SGPR_CLOBBER)}\n"
+            f"#define HARP_FWD_ASM_LOOP \\\n{body(lines)}\n")
 
 
 def write(path=None):
     path = path or os.path.join(os.path.dirname(os.path.abspath(__file__)), "fwd_asm.inc")
-    text = render(build(), build(probe=True))
+    text = render(build())
     old = open(path).read() if os.path.exists(path) else None
     if old != text:
         with open(path, "w") as f:
