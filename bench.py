@@ -338,6 +338,237 @@ def producer_cpu_baseline(cfg, seed: int, target_s: float = 4.0):
             "sample": f"{rows} rows of D={D} (fused forward + backward, numpy), {dt:.1f} s on {cpu_model()}"}
 
 
+PROBE_LIB = os.path.join(os.path.dirname(os.path.abspath(__file__)), "kernels", "libharp_bench_probe.so")
+_probe_lib = None
+
+
+def probe_rate(lds_fed: bool, iters: int, seed: int) -> tuple:
+    """(TFLOP/s, shader GHz) of a dense bf16 MFMA stream on random operands
+    (bench_probe.hip): register-fed at 32 waves per CU, or (lds_fed) with
+    one operand of every MFMA read from LDS at the kernels' 8 waves per CU."""
+    import ctypes
+
+    global _probe_lib
+    if _probe_lib is None:
+        if not os.path.exists(PROBE_LIB):
+            raise FileNotFoundError(f"{PROBE_LIB} is not built: run __graft_entry__.build()")
+        lib = ctypes.CDLL(PROBE_LIB)
+        for fn in (lib.harp_probe_mfma_rate, lib.harp_probe_mfma_lds_rate):
+            fn.restype = ctypes.c_int
+            fn.argtypes = [ctypes.c_int, ctypes.c_uint32, ctypes.POINTER(ctypes.c_double),
+                           ctypes.POINTER(ctypes.c_double)]
+        lib.harp_probe_last_error.restype = ctypes.c_char_p
+        _probe_lib = lib
+    tf, ghz = ctypes.c_double(), ctypes.c_double()
+    fn = _probe_lib.harp_probe_mfma_lds_rate if lds_fed else _probe_lib.harp_probe_mfma_rate
+    rc = fn(int(iters), int(seed) & 0xFFFFFFFF, ctypes.byref(tf), ctypes.byref(ghz))
+    if rc != 0:
+        raise RuntimeError(f"MFMA probe failed (status {rc}): {_probe_lib.harp_probe_last_error().decode()}")
+    return tf.value, ghz.value
+
+
+class BoardTelemetry:
+    """The board's own power, shader-clock and power-limit readings (SMU
+    metrics through amdsmi), taken while one piece of work runs in a loop:
+    socket power and GFX clock sampled every few milliseconds, the average
+    power from the energy counter, and the share of the interval the SMU
+    spent limiting the clock for package power (PPT residency counters).
+    Read-only; every field is None where this board or driver does not
+    report it."""
+
+    def __init__(self, torch_mod):
+        import amdsmi
+
+        self.smi = amdsmi
+        amdsmi.amdsmi_init()
+        handles = amdsmi.amdsmi_get_processor_handles()
+        if not handles:
+            raise RuntimeError("amdsmi sees no GPU")
+        self.h = handles[0]
+        props = torch_mod.cuda.get_device_properties(0)
+        bus = getattr(props, "pci_bus_id", None)
+        if bus is not None and len(handles) > 1:
+            for h in handles:
+                try:
+                    bdf = amdsmi.amdsmi_get_gpu_device_bdf(h)
+                    if int(bdf.split(":")[1], 16) == int(bus):
+                        self.h = h
+                        break
+                except Exception:  # noqa: BLE001 - best effort matching
+                    pass
+        self.cap_w = None
+        try:
+            cap = amdsmi.amdsmi_get_power_cap_info(self.h).get("power_cap")
+            if isinstance(cap, (int, float)) and cap > 0:
+                self.cap_w = cap / 1e6 if cap > 1e5 else float(cap)  # reported in microwatts
+        except Exception:  # noqa: BLE001
+            pass
+
+    def _metrics(self):
+        return self.smi.amdsmi_get_gpu_metrics_info(self.h)
+
+    @staticmethod
+    def _num(x):
+        return x if isinstance(x, (int, float)) and not isinstance(x, bool) else None
+
+    def measure(self, fn, seconds: float, sync) -> dict:
+        import statistics
+        import threading
+
+        samples = []
+        stop = threading.Event()
+
+        def sampler():
+            while not stop.is_set():
+                try:
+                    m = self._metrics()
+                    clks = m.get("current_gfxclks")
+                    clk = None
+                    if isinstance(clks, (list, tuple)):
+                        v = [c for c in clks if self._num(c) and 0 < c < 10000]
+                        clk = sum(v) / len(v) if v else None
+                    if clk is None:
+                        clk = self._num(m.get("current_gfxclk"))
+                    samples.append((self._num(m.get("current_socket_power")), clk))
+                except Exception:  # noqa: BLE001
+                    pass
+                stop.wait(0.005)
+
+        m0 = self._metrics()
+        t0 = time.perf_counter()
+        th = threading.Thread(target=sampler, daemon=True)
+        th.start()
+        n = 0
+        while time.perf_counter() - t0 < seconds:
+            fn()
+            n += 1
+            sync()
+        stop.set()
+        th.join()
+        t1 = time.perf_counter()
+        m1 = self._metrics()
+
+        def delta(key):
+            a, b = self._num(m0.get(key)), self._num(m1.get(key))
+            return None if a is None or b is None else b - a
+
+        acc = delta("accumulation_counter")
+        ppt = delta("ppt_residency_acc")
+        thm = delta("socket_thm_residency_acc")
+        pw = [p for p, _ in samples if p]
+        ck = [c for _, c in samples if c]
+        return {
+            "seconds": round(t1 - t0, 3),
+            "calls": n,
+            "samples": len(samples),
+            "socket_power_w_median": round(statistics.median(pw), 1) if pw else None,
+            "socket_power_w_max": round(max(pw), 1) if pw else None,
+            "power_cap_w": round(self.cap_w, 1) if self.cap_w else None,
+            "gfxclk_mhz_median": round(statistics.median(ck), 1) if ck else None,
+            "gfxclk_mhz_min": round(min(ck), 1) if ck else None,
+            "ppt_limited_frac": round(min(1.0, max(0.0, ppt / acc)), 4) if acc and ppt is not None else None,
+            "thermal_limited_frac": round(min(1.0, max(0.0, thm / acc)), 4) if acc and thm is not None else None,
+        }
+
+
+def bhtld_of(cfg) -> float:
+    lens = cfg["lens"]
+    L = sum(lens) if lens else cfg["N"] * cfg["tc"]
+    return float(cfg["B"]) * cfg["H"] * cfg["T"] * L * cfg["D"]
+
+
+class Workload:
+    """One BASELINE config resident on the device, with the step of the hot
+    path (forward, delta, backward through torch.ops.ring_attention_ops)."""
+
+    def __init__(self, cfg, seed, dev):
+        import torch
+
+        self.cfg = cfg
+        B, H, T, D, N, tc = cfg["B"], cfg["H"], cfg["T"], cfg["D"], cfg["N"], cfg["tc"]
+        self.lens, self.N, self.tc = cfg["lens"], N, tc
+        self.scale = 1.0 / math.sqrt(D)
+        self.q, self.k, self.v, self.do = make_inputs_dev(cfg, seed, dev)
+        self.out = torch.empty((B, T, H, D), device=dev, dtype=torch.float32).transpose(1, 2)
+        self.m_i = torch.empty((B, H, T, 1), device=dev, dtype=torch.bfloat16)
+        self.l_i = torch.empty((B, H, T, 1), device=dev, dtype=torch.float32)
+        self.dq = torch.empty_like(self.q)
+        self.dk = torch.empty_like(self.k)
+        self.dv = torch.empty_like(self.v)
+        self.delta = None
+        self.ops = torch.ops.ring_attention_ops
+
+    def forward(self):
+        self.ops.ring_attention_forward(self.q, self.k, self.v, self.out, self.m_i, self.l_i, self.N, self.scale, 0,
+                                        self.lens, self.tc)
+
+    def backward(self):
+        self.delta = self.ops.ring_attention_delta(self.do, self.out)
+        self.ops.ring_attention_backward(self.q, self.dq, self.k, self.dk, self.v, self.dv, self.do, self.m_i,
+                                         self.l_i, self.delta, self.N, self.scale, 0, self.lens, self.tc)
+
+    def step(self):
+        self.forward()
+        self.backward()
+
+    def timed(self, steps: int, warmup: int) -> dict:
+        """warmup untimed steps, then `steps` timed ones (HIP events on the
+        current stream, one per step) with the library's per-kernel launch
+        timing on; returns ms per step (mean and median), per-kernel (ms,
+        launches) and the host wall time of the timed region."""
+        import torch
+
+        from harp_amd import _lib
+
+        for _ in range(warmup):
+            self.step()
+        torch.cuda.synchronize()
+        _lib.timing_read()  # discard
+        _lib.timing_enable(True)
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+        torch.cuda.synchronize()
+        t_wall = time.perf_counter()
+        ev[0].record()
+        for i in range(steps):
+            self.step()
+            ev[i + 1].record()
+        torch.cuda.synchronize()
+        wall_s = time.perf_counter() - t_wall
+        _lib.timing_enable(False)
+        kt = _lib.timing_read()
+        step_ms = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(steps))
+        med = step_ms[len(step_ms) // 2] if len(step_ms) % 2 else 0.5 * (
+            step_ms[len(step_ms) // 2 - 1] + step_ms[len(step_ms) // 2])
+        return {"ms": ev[0].elapsed_time(ev[-1]) / steps, "median_ms": med, "kernels": kt, "wall_s": wall_s}
+
+
+def other_configs(ids, seed, dev, steps: int = 10, warmup: int = 3) -> dict:
+    """The other BASELINE configs that run on the GPU (parity cases, not the
+    headline): ms per fwd+bwd step, counted TFLOP/s and % of the bf16 peak,
+    and each kernel's ms per step."""
+    import torch
+
+    res = {}
+    for cid in ids:
+        cfg = CONFIGS[cid]
+        w = Workload(cfg, seed, dev)
+        r = w.timed(steps, warmup)
+        tf = 14.0 * bhtld_of(cfg) / (r["ms"] * 1e-3) / 1e12
+        res[str(cid)] = {
+            "shape": f"B{cfg['B']} H{cfg['H']} D{cfg['D']} T{cfg['T']}, {cfg['N']} chunks of {cfg['tc']}"
+                     + (f" ({cfg['lens'][0]} valid, pad keys masked)" if cfg["lens"] else ""),
+            "ms_per_step": round(r["ms"], 4),
+            "tflops": round(tf, 1),
+            "pct_bf16_peak": round(100.0 * tf / PEAK_BF16_TFLOPS, 2),
+            "kernel_ms_per_step": {k: round(ms / steps, 4) for k, (ms, n) in r["kernels"].items() if n},
+            "steps": steps,
+        }
+        del w
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -349,6 +580,9 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-producer", action="store_true",
                     help="skip the QK RMSNorm + RoPE (producer step) measurement")
+    ap.add_argument("--no-telemetry", action="store_true", help="skip the board power / clock readings")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="skip BASELINE configs 2, 3 and 5 after the headline (config 4) run")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="before the timed steps, run one plain device copy of this many MiB "
                          "(a known-size reference for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -362,31 +596,17 @@ def main() -> int:
     import torch
 
     import harp_amd
-    from harp_amd import _lib
 
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     harp_amd.load_ops()
-    ops = torch.ops.ring_attention_ops
 
     cfg = CONFIGS[args.config]
     B, H, T, D, N, tc = cfg["B"], cfg["H"], cfg["T"], cfg["D"], cfg["N"], cfg["tc"]
     lens = cfg["lens"]
     L = sum(lens) if lens else N * tc
-    scale = 1.0 / math.sqrt(D)
-    q, k, v, do = make_inputs_dev(cfg, args.seed, dev)
-    out = torch.empty((B, T, H, D), device=dev, dtype=torch.float32).transpose(1, 2)
-    m_i = torch.empty((B, H, T, 1), device=dev, dtype=torch.bfloat16)
-    l_i = torch.empty((B, H, T, 1), device=dev, dtype=torch.float32)
-    dq = torch.empty_like(q)
-    dk = torch.empty_like(k)
-    dv = torch.empty_like(v)
-
-    def step():
-        ops.ring_attention_forward(q, k, v, out, m_i, l_i, N, scale, 0, lens, tc)
-        delta = ops.ring_attention_delta(do, out)
-        ops.ring_attention_backward(q, dq, k, dk, v, dv, do, m_i, l_i, delta, N, scale, 0, lens, tc)
+    work = Workload(cfg, args.seed, dev)
 
     if args.copy_calibration_mib > 0:
         n = args.copy_calibration_mib * (1 << 20) // 4
@@ -397,28 +617,11 @@ def main() -> int:
         torch.cuda.synchronize()
         del src, dst
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    _lib.timing_read()  # discard
-    _lib.timing_enable(True)
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
-    torch.cuda.synchronize()
-    t_wall = time.perf_counter()
-    ev[0].record()
-    for i in range(args.steps):
-        step()
-        ev[i + 1].record()
-    torch.cuda.synchronize()
-    wall_s = time.perf_counter() - t_wall
-    _lib.timing_enable(False)
-    kt = _lib.timing_read()
-    ms_per_step = ev[0].elapsed_time(ev[-1]) / args.steps
-    step_ms = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(args.steps))
-    ms_median = step_ms[len(step_ms) // 2] if len(step_ms) % 2 else 0.5 * (
-        step_ms[len(step_ms) // 2 - 1] + step_ms[len(step_ms) // 2])
+    r = work.timed(args.steps, args.warmup)
+    kt, wall_s, ms_per_step, ms_median = r["kernels"], r["wall_s"], r["ms"], r["median_ms"]
+    print(f"bench: config {args.config} timed, {ms_per_step:.4f} ms per step", file=sys.stderr, flush=True)
 
-    bhtld = float(B) * H * T * L * D
+    bhtld = bhtld_of(cfg)
     flop_total = 14.0 * bhtld
     tflops = flop_total / (ms_per_step * 1e-3) / 1e12
     # algorithmic MFMA work per launch in this design's accounting
@@ -426,20 +629,10 @@ def main() -> int:
     # MFMA work each kernel performs (dq recomputes S and dP: 4 more units)
     kernel_mfma = {"fwd": 4.0 * bhtld, "dkdv": 8.0 * bhtld, "dq": 6.0 * bhtld}
     # sustained MFMA rate of this board (register-fed bf16 MFMA stream on
-    # random operands): what the power limit lets any MFMA-bound kernel reach
-    probe_tf, probe_ghz = _lib.probe_mfma_rate(4096, args.seed)
-    # the same at the kernels' operand path: one operand of every MFMA from
-    # LDS (1 KB per MFMA per wave, 8 waves per CU); the LDS reads draw power
-    # from the MFMA stream, so this is the ceiling for this kernel design
-    lds_tf, lds_ghz = _lib.probe_mfma_lds_rate(False, 32768, args.seed)
-    # and at each kernel's own instruction mix: the same LDS-fed stream plus
-    # the kernel's measured VALU / exp / copy work per MFMA, with nothing
-    # waiting on anything -- the rate that mix allows on this board
-    mix = {k: _lib.probe_kernel_mix(k, 24576, args.seed) for k in kernel_mfma}
-    if D == 128:  # the three kernels run hand-scheduled loops: their ceilings are those loops' steady states
-        mix["fwd"] = _lib.probe_fwd_asm_loop(4096, args.seed)
-        mix["dq"] = _lib.probe_dq_asm_loop(4096, args.seed)
-        mix["dkdv"] = _lib.probe_dkdv_asm_loop(4096, args.seed)
+    # random operands), and the same at the kernels' operand path (one
+    # operand of every MFMA from LDS, 1 KB per MFMA per wave, 8 waves per CU)
+    probe_tf, probe_ghz = probe_rate(False, 4096, args.seed)
+    lds_tf, lds_ghz = probe_rate(True, 32768, args.seed)
     kernels = {}
     for name, (ms, n) in kt.items():
         if n:
@@ -451,10 +644,6 @@ def main() -> int:
                 entry["tflops_mfma_performed"] = round(performed, 1)
                 entry["frac_of_sustained"] = round(performed / probe_tf, 4) if probe_tf > 0 else None
                 entry["frac_of_lds_fed"] = round(performed / lds_tf, 4) if lds_tf > 0 else None
-                mix_tf, mix_ghz = mix[name]
-                entry["mix_ceiling_tflops"] = round(mix_tf, 1)
-                entry["mix_ceiling_shader_ghz"] = round(mix_ghz, 3)
-                entry["frac_of_mix_ceiling"] = round(performed / mix_tf, 4) if mix_tf > 0 else None
             kernels[name] = entry
     dom = max((n for n in kernel_flops if n in kernels), key=lambda n: kt[n][0])
     dom_tf = kernels[dom]["tflops_algorithmic"]
@@ -499,13 +688,35 @@ def main() -> int:
             "lds_fed_mfma_tflops": round(lds_tf, 1),
             "lds_fed_mfma_shader_ghz": round(lds_ghz, 3),
             "frac_of_lds_fed": round(dom_tf / lds_tf, 4) if lds_tf > 0 else None,
-            "mix_ceiling_tflops": kernels[dom]["mix_ceiling_tflops"],
-            "frac_of_mix_ceiling": kernels[dom]["frac_of_mix_ceiling"],
         },
         "cpu_baseline": None,
         "gpu": torch.cuda.get_device_name(0),
         "clock_policy": "default power mode (not pinned)",
     }
+    if not args.no_telemetry:
+        # the board's power / clock / power-limit readings while each piece
+        # of work runs alone in a loop (after the timed steps, outside them)
+        try:
+            tel = BoardTelemetry(torch)
+            sync = torch.cuda.synchronize
+            result["telemetry"] = {
+                "probe_register_fed": tel.measure(lambda: probe_rate(False, 65536, args.seed), 1.5, sync),
+                "probe_lds_fed": tel.measure(lambda: probe_rate(True, 262144, args.seed), 1.5, sync),
+                "forward": tel.measure(work.forward, 1.5, sync),
+                "backward_dkdv_dq": tel.measure(work.backward, 1.5, sync),
+                "what": "amdsmi SMU metrics while the work runs in a loop: socket power and GFX clock sampled "
+                        "every ~5 ms (median, max / min), ppt_limited_frac = share of the interval the SMU held "
+                        "the clock down for package power (ppt_residency_acc / accumulation_counter deltas)",
+            }
+        except Exception as e:  # noqa: BLE001 - telemetry is context, never the measurement
+            result["telemetry"] = {"unavailable": f"{type(e).__name__}: {e}"}
+        print("bench: telemetry done", file=sys.stderr, flush=True)
+    if args.config == 4 and not args.no_other_configs:
+        del work
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        result["other_configs"] = other_configs((2, 3, 5), args.seed, dev)
+        print("bench: other configs done", file=sys.stderr, flush=True)
     if not args.no_producer:
         prod = producer_bench(cfg, args.seed)
         rows = B * H * T

@@ -21,7 +21,6 @@ KERNELS = ROOT / "kernels"
 ABI_LIB = KERNELS / "libharp_ra.so"
 OPS_LIB = KERNELS / "libring_attention_ops.so"
 ASYNC_OPS_LIB = KERNELS / "libharp_async_op.so"
-PROBE_LIB = KERNELS / "libharp_probe.so"  # bench-only measurement aid, not a drop-in library
 
 HARP_RA_OK = 0
 HARP_RA_EINVAL = 1
@@ -35,7 +34,6 @@ KERNEL_KINDS = ("stats", "fwd", "delta", "dkdv", "dq")
 
 _lock = threading.Lock()
 _abi: ctypes.CDLL | None = None
-_probe: ctypes.CDLL | None = None
 _ops_loaded = False
 _async_ops_loaded = False
 
@@ -181,124 +179,6 @@ def ptr_array(ptrs) -> ctypes.Array:
 
 def i32_array(vals) -> ctypes.Array:
     return (ctypes.c_int32 * len(vals))(*[int(v) for v in vals])
-
-
-def load_probe() -> ctypes.CDLL:
-    """Open kernels/libharp_probe.so, the bench-only sustained-MFMA probe."""
-    global _probe
-    with _lock:
-        if _probe is None:
-            if not PROBE_LIB.exists():
-                raise _missing(PROBE_LIB)
-            lib = ctypes.CDLL(str(PROBE_LIB))
-            lib.harp_probe_mfma_rate.restype = _i
-            lib.harp_probe_mfma_rate.argtypes = [_i, ctypes.c_uint32, ctypes.POINTER(ctypes.c_double),
-                                                 ctypes.POINTER(ctypes.c_double)]
-            lib.harp_probe_mfma_lds_rate.restype = _i
-            lib.harp_probe_mfma_lds_rate.argtypes = [_i, ctypes.c_uint32, _i, ctypes.POINTER(ctypes.c_double),
-                                                     ctypes.POINTER(ctypes.c_double)]
-            lib.harp_probe_kernel_mix.restype = _i
-            lib.harp_probe_kernel_mix.argtypes = [_i, _i, ctypes.c_uint32, ctypes.POINTER(ctypes.c_double),
-                                                  ctypes.POINTER(ctypes.c_double)]
-            lib.harp_probe_fwd_asm_loop.restype = _i
-            lib.harp_probe_fwd_asm_loop.argtypes = [_i, ctypes.c_uint32, ctypes.POINTER(ctypes.c_double),
-                                                    ctypes.POINTER(ctypes.c_double)]
-            lib.harp_probe_dkdv_asm_loop.restype = _i
-            lib.harp_probe_dkdv_asm_loop.argtypes = [_i, ctypes.c_uint32, ctypes.POINTER(ctypes.c_double),
-                                                     ctypes.POINTER(ctypes.c_double)]
-            lib.harp_probe_dq_asm_loop.restype = _i
-            lib.harp_probe_dq_asm_loop.argtypes = [_i, ctypes.c_uint32, ctypes.POINTER(ctypes.c_double),
-                                                   ctypes.POINTER(ctypes.c_double)]
-            lib.harp_probe_last_error.restype = ctypes.c_char_p
-            lib.harp_probe_last_error.argtypes = []
-            _probe = lib
-        return _probe
-
-
-def probe_mfma_rate(iters: int = 4096, seed: int = 3407) -> tuple:
-    """(TFLOP/s, shader GHz) of a register-fed bf16 MFMA stream on random
-    operands: the sustained MFMA rate of this device under its power limit."""
-    lib = load_probe()
-    tf = ctypes.c_double()
-    ghz = ctypes.c_double()
-    rc = lib.harp_probe_mfma_rate(int(iters), int(seed) & 0xFFFFFFFF, ctypes.byref(tf), ctypes.byref(ghz))
-    if rc != 0:
-        raise RuntimeError(f"harp_probe_mfma_rate failed (status {rc}): {lib.harp_probe_last_error().decode()}")
-    return tf.value, ghz.value
-
-
-def probe_mfma_lds_rate(softmax: bool, iters: int = 8192, seed: int = 3407) -> tuple:
-    """(TFLOP/s, shader GHz) of the same MFMA stream at the attention kernels'
-    occupancy (8 waves per CU) with one operand of every MFMA read from LDS
-    (1 KB per MFMA per wave), and with softmax=True one exp and three FMAs per
-    MFMA besides: the rate that operand path allows under the power limit."""
-    lib = load_probe()
-    tf = ctypes.c_double()
-    ghz = ctypes.c_double()
-    rc = lib.harp_probe_mfma_lds_rate(int(iters), int(seed) & 0xFFFFFFFF, 1 if softmax else 0, ctypes.byref(tf),
-                                      ctypes.byref(ghz))
-    if rc != 0:
-        raise RuntimeError(f"harp_probe_mfma_lds_rate failed (status {rc}): {lib.harp_probe_last_error().decode()}")
-    return tf.value, ghz.value
-
-
-PROBE_KERNELS = {"fwd": 0, "dkdv": 1, "dq": 2}
-
-
-def probe_kernel_mix(kernel: str, iters: int = 24576, seed: int = 3407) -> tuple:
-    """(TFLOP/s, shader GHz) of the LDS-fed MFMA stream carrying one attention
-    kernel's measured per-MFMA work besides (VALU instructions, exps and
-    direct-to-LDS copy bytes; kernel "fwd", "dkdv" or "dq"), with no
-    dependency between the streams: the rate that instruction mix allows on
-    this board under its power limit."""
-    lib = load_probe()
-    tf = ctypes.c_double()
-    ghz = ctypes.c_double()
-    rc = lib.harp_probe_kernel_mix(PROBE_KERNELS[kernel], int(iters), int(seed) & 0xFFFFFFFF, ctypes.byref(tf),
-                                   ctypes.byref(ghz))
-    if rc != 0:
-        raise RuntimeError(f"harp_probe_kernel_mix failed (status {rc}): {lib.harp_probe_last_error().decode()}")
-    return tf.value, ghz.value
-
-
-def probe_fwd_asm_loop(key_blocks: int = 4096, seed: int = 3407) -> tuple:
-    """(TFLOP/s, shader GHz) of the D = 128 forward's own generated loop
-    (fwd_asm.inc) run on synthetic keys for `key_blocks` 32-key blocks, one
-    4-wave block per CU: the steady-state ceiling of fwd_asm_kernel."""
-    lib = load_probe()
-    tf = ctypes.c_double()
-    ghz = ctypes.c_double()
-    rc = lib.harp_probe_fwd_asm_loop(int(key_blocks), int(seed) & 0xFFFFFFFF, ctypes.byref(tf), ctypes.byref(ghz))
-    if rc != 0:
-        raise RuntimeError(f"harp_probe_fwd_asm_loop failed (status {rc}): {lib.harp_probe_last_error().decode()}")
-    return tf.value, ghz.value
-
-
-def probe_dq_asm_loop(key_blocks: int = 4096, seed: int = 3407) -> tuple:
-    """(TFLOP/s, shader GHz) of the D = 128 dQ kernel's own generated loop
-    (dq_asm.inc) run on synthetic keys for `key_blocks` 32-key blocks, one
-    4-wave block per CU: the steady-state ceiling of dq_asm_kernel."""
-    lib = load_probe()
-    tf = ctypes.c_double()
-    ghz = ctypes.c_double()
-    rc = lib.harp_probe_dq_asm_loop(int(key_blocks), int(seed) & 0xFFFFFFFF, ctypes.byref(tf), ctypes.byref(ghz))
-    if rc != 0:
-        raise RuntimeError(f"harp_probe_dq_asm_loop failed (status {rc}): {lib.harp_probe_last_error().decode()}")
-    return tf.value, ghz.value
-
-
-def probe_dkdv_asm_loop(query_blocks: int = 4096, seed: int = 3407) -> tuple:
-    """(TFLOP/s, shader GHz) of the D = 128 dK/dV kernel's own generated loop
-    (dkdv_asm.inc) run on one synthetic query block for `query_blocks`
-    32-query blocks, one 4-wave block per CU: the steady-state ceiling of
-    dkdv_asm_kernel."""
-    lib = load_probe()
-    tf = ctypes.c_double()
-    ghz = ctypes.c_double()
-    rc = lib.harp_probe_dkdv_asm_loop(int(query_blocks), int(seed) & 0xFFFFFFFF, ctypes.byref(tf), ctypes.byref(ghz))
-    if rc != 0:
-        raise RuntimeError(f"harp_probe_dkdv_asm_loop failed (status {rc}): {lib.harp_probe_last_error().decode()}")
-    return tf.value, ghz.value
 
 
 def timing_enable(on: bool) -> None:

@@ -13,9 +13,6 @@ so the operator libraries find the C-ABI library through ``$ORIGIN``):
 * ``libharp_async_op.so``        the PyTorch operator library for the QK RMSNorm
                                  and RoPE operators (namespace ``async_op``,
                                  async_rt/csrc/async_op_api.cc:54-57), on the GPU.
-* ``libharp_probe.so``           bench-only: the sustained-MFMA probe bench.py
-                                 reports beside its roofline (not a drop-in
-                                 library; nothing on the operator path loads it).
 
 Run ``python -m harp_amd.build`` (or ``__graft_entry__.build()``).
 """
@@ -34,10 +31,8 @@ OUT = ROOT / "kernels"
 ABI_LIB = OUT / "libharp_ra.so"
 OPS_LIB = OUT / "libring_attention_ops.so"
 ASYNC_OPS_LIB = OUT / "libharp_async_op.so"
-PROBE_LIB = OUT / "libharp_probe.so"
 
 HIP_SOURCES = ["ra_kernels.hip", "fwd_asm.hip", "dq_asm.hip", "dkdv_asm.hip", "ra_abi.hip", "qk_kernels.hip", "qk_abi.hip", "proj_kernels.hip"]
-PROBE_SOURCE = "bench/mfma_probe.hip"
 HIP_HEADERS = ["ra_common.h", "ra_kernels.h", "qk_kernels.h", "proj_kernels.h", "fwd_asm.inc", "fwd_asm_gen.py",
                "dq_asm.inc", "dq_asm_gen.py", "dkdv_asm.inc",
                "dkdv_asm_gen.py", "asm_sched.py"]
@@ -100,15 +95,6 @@ def build_abi(verbose: bool = False) -> Path:
     return ABI_LIB
 
 
-def build_probe(verbose: bool = False) -> Path:
-    """kernels/libharp_probe.so: the bench-only sustained-MFMA probe."""
-    OUT.mkdir(parents=True, exist_ok=True)
-    tmp = PROBE_LIB.with_suffix(".so.tmp")
-    _run([str(ROCM / "bin" / "hipcc"), *HIPCC_FLAGS, str(CSRC / PROBE_SOURCE), "-o", str(tmp)], verbose)
-    os.replace(tmp, PROBE_LIB)
-    return PROBE_LIB
-
-
 def build_ops(verbose: bool = False, source: str = OPS_SOURCE, lib: Path = OPS_LIB,
               ext_name: str = "ring_attention_ops") -> Path:
     import torch.utils.cpp_extension as ce
@@ -159,16 +145,15 @@ def build(verbose: bool = False) -> None:
     build_abi(verbose)
     build_ops(verbose)
     build_async_ops(verbose)
-    build_probe(verbose)
 
 
 def sources_newer_than_libs() -> bool:
     """True when a source file is newer than a built library (or one is missing)."""
-    libs = [ABI_LIB, OPS_LIB, ASYNC_OPS_LIB, PROBE_LIB]
+    libs = [ABI_LIB, OPS_LIB, ASYNC_OPS_LIB]
     if not all(p.exists() for p in libs):
         return True
     newest_lib = min(p.stat().st_mtime for p in libs)
-    srcs = [CSRC / s for s in HIP_SOURCES + HIP_HEADERS + [OPS_SOURCE, ASYNC_OPS_SOURCE, PROBE_SOURCE]]
+    srcs = [CSRC / s for s in HIP_SOURCES + HIP_HEADERS + [OPS_SOURCE, ASYNC_OPS_SOURCE]]
     srcs += [INCLUDE / "harp_ring_attn.h", INCLUDE / "harp_qk_norm_rope.h"]
     return any(s.stat().st_mtime > newest_lib for s in srcs)
 

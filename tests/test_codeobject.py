@@ -43,7 +43,8 @@ def kernel_notes(lib_path):
 
 
 @pytest.mark.skipif(not os.path.exists(f"{LLVM}/clang-offload-bundler"), reason="ROCm LLVM tools not installed")
-@pytest.mark.parametrize("lib", [_lib.ABI_LIB, _lib.PROBE_LIB], ids=["libharp_ra", "libharp_probe"])
+@pytest.mark.parametrize("lib", [_lib.ABI_LIB, _lib.KERNELS / "libharp_bench_probe.so"],
+                         ids=["libharp_ra", "libharp_bench_probe"])
 def test_no_scratch_and_no_spills(lib):
     if not lib.exists():
         pytest.skip(f"{lib} not built")
