@@ -492,20 +492,22 @@ int harp_ra_backward(const void* q, const int64_t* q_strides, void* grad_q, cons
   if (dkv_dtype != HARP_RA_F32 && dkv_dtype != HARP_RA_BF16)
     return fail(HARP_RA_EINVAL, "dkv_dtype must be F32 or BF16");
   if (!k_chunks || !v_chunks || !dk_chunks || !dv_chunks) return fail(HARP_RA_EINVAL, "chunk pointer arrays are NULL");
-  // bf16 dK / dV rows are written four elements (8 bytes) per lane store
-  if (dkv_dtype == HARP_RA_BF16)
+  // at head dim 128 the dK / dV kernel writes bf16 rows four elements (8
+  // bytes) per lane store; the kernel for other head dims stores elements
+  const bool dkv_wide = dkv_dtype == HARP_RA_BF16 && h_len == 128;
+  if (dkv_wide)
     for (int i = 0; i < 3; ++i)
       if (dkv_strides && dkv_strides[i] % 4 != 0)
-        return fail(HARP_RA_EINVAL, "bf16 dK / dV stride[%d]=%lld must be a multiple of 4 elements", i,
+        return fail(HARP_RA_EINVAL, "bf16 dK / dV stride[%d]=%lld must be a multiple of 4 elements at h_len 128", i,
                     (long long)dkv_strides[i]);
   for (int c = 0; c < sp_size; ++c) {
     if ((rc = check_bf16_view(k_chunks[c], kv_strides, h_len, "k chunk"))) return rc;
     if ((rc = check_bf16_view(v_chunks[c], kv_strides, h_len, "v chunk"))) return rc;
     if ((rc = check_out_view(dk_chunks[c], dkv_strides, batch, h_num, kv_chunk_len, h_len, "dK chunk"))) return rc;
     if ((rc = check_out_view(dv_chunks[c], dkv_strides, batch, h_num, kv_chunk_len, h_len, "dV chunk"))) return rc;
-    if (dkv_dtype == HARP_RA_BF16 &&
+    if (dkv_wide &&
         ((reinterpret_cast<uintptr_t>(dk_chunks[c]) | reinterpret_cast<uintptr_t>(dv_chunks[c])) & 7u) != 0)
-      return fail(HARP_RA_EINVAL, "bf16 dK / dV chunks must be 8-byte aligned");
+      return fail(HARP_RA_EINVAL, "bf16 dK / dV chunks must be 8-byte aligned at h_len 128");
   }
   if ((rc = check_extent(kv_chunk_len, kv_strides, "k/v chunk"))) return rc;
   if ((rc = check_extent(t_num, q_strides, "q"))) return rc;

@@ -13,6 +13,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "acc_layout.h"
+
 namespace harp_ra {
 
 typedef __bf16 bf16;
@@ -86,8 +88,8 @@ __device__ __forceinline__ int lane_id_fresh() {
   return l;
 }
 
-// Row of the 32x32 C layout held in accumulator register r by lane-half g.
-__device__ __forceinline__ constexpr int c_row(int r, int g) { return 8 * (r >> 2) + 4 * g + (r & 3); }
+// c_row(r, g): row of the 32x32 C layout held in accumulator register r by
+// lane-half g (acc_layout.h, shared with host code).
 
 // ---------------------------------------------------------------------------
 // Direct-to-LDS copies through buffer descriptors

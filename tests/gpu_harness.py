@@ -36,9 +36,14 @@ def run_hip(
     do_layout: str = "token",
     grad_dtype: torch.dtype = torch.bfloat16,
     backward: bool = True,
+    dkv_view: Optional[tuple] = None,
 ) -> Dict[str, torch.Tensor]:
     """Run forward (+ delta + backward) on the GPU; return CPU tensors:
-    o (fp32), lse (fp64), m, l, delta, dq, dk, dv (dk/dv concatenated over chunks)."""
+    o (fp32), lse (fp64), m, l, delta, dq, dk, dv (dk/dv concatenated over chunks).
+    dkv_view = (pad, offset) (C ABI only): each dK / dV chunk is the view
+    [..., offset:offset + D] of a token-major buffer whose rows hold D + pad
+    elements per head, so the view's row stride is H (D + pad) and its base
+    sits `offset` elements into the buffer."""
     dev = torch.device("cuda")
     B, H, T, D = q.shape
     n = len(ks)
@@ -71,15 +76,22 @@ def run_hip(
             delta = torch.empty((B, H, T, 1), device=dev, dtype=torch.float32)
             hops.abi_delta(dod, out, delta)
             dq = torch.full((B, T, H, D), float("nan"), device=dev, dtype=grad_dtype).transpose(1, 2)
-            dk = [torch.full((B, tc, H, D), float("nan"), device=dev, dtype=grad_dtype).transpose(1, 2)
-                  for _ in range(n)]
-            dv = [torch.full((B, tc, H, D), float("nan"), device=dev, dtype=grad_dtype).transpose(1, 2)
-                  for _ in range(n)]
+
+            def grad_chunk():
+                if dkv_view is not None:
+                    pad, off = dkv_view
+                    buf = torch.full((B, tc, H, D + pad), float("nan"), device=dev, dtype=grad_dtype)
+                    return buf[..., off:off + D].transpose(1, 2)
+                return torch.full((B, tc, H, D), float("nan"), device=dev, dtype=grad_dtype).transpose(1, 2)
+
+            dk = [grad_chunk() for _ in range(n)]
+            dv = [grad_chunk() for _ in range(n)]
             hops.abi_backward(qd, dq, kd, vd, dk, dv, dod, m_i, l_i, delta, scale, ring_rank=ring_rank,
                               kv_lens=kv_lens)
             dk_all = torch.cat(dk, dim=2)
             dv_all = torch.cat(dv, dim=2)
         else:
+            assert dkv_view is None, "dkv_view goes through the C ABI"
             delta = torch.ops.ring_attention_ops.ring_attention_delta(dod, out)
             dq = torch.full((B, T, H, D), float("nan"), device=dev, dtype=grad_dtype).transpose(1, 2)
             dk_all = torch.full((B, n * tc, H, D), float("nan"), device=dev, dtype=grad_dtype).transpose(1, 2)

@@ -149,6 +149,9 @@ def test_product_package_never_imports_the_oracle():
                 assert "oracle" not in text.replace("oracle/", "").lower() or fn == "build.py", fn
 
 
+_ST128 = _lib.i64_array([8 * 128 * 128, 128, 8 * 128, 1])
+
+
 def _bwd_call(**over):
     lib = harp_amd.load_abi()
     st = _lib.i64_array([8 * 64 * 128, 64, 8 * 64, 1])
@@ -171,14 +174,29 @@ def _bwd_call(**over):
         (dict(ks=_lib.i64_array([0, 0, 0, 1])), "k chunk row stride"),
         (dict(dqs=_lib.i64_array([8 * 64 * 128, 64, 0, 1])), "grad_q strides make elements overlap"),
         (dict(dks=_lib.i64_array([8 * 64 * 128, 0, 8 * 64, 1])), "dK chunk strides make elements overlap"),
-        # bf16 dK / dV rows are stored 8 bytes per lane
-        (dict(dks=_lib.i64_array([8 * 66 * 128, 66, 8 * 66 + 2, 1])), "must be a multiple of 4 elements"),
-        (dict(dkc=_lib.ptr_array([(1 << 20) + 2])), "must be 8-byte aligned"),
+        # bf16 dK / dV rows at head dim 128 are stored 8 bytes per lane
+        (dict(D=128, qs=_ST128, dqs=_ST128, ks=_ST128, dos=_ST128,
+              dks=_lib.i64_array([8 * 130 * 128, 130, 8 * 130, 1])), "must be a multiple of 4 elements"),
+        (dict(D=128, qs=_ST128, dqs=_ST128, ks=_ST128, dos=_ST128, dks=_ST128,
+              dkc=_lib.ptr_array([(1 << 20) + 2])), "must be 8-byte aligned"),
     ],
 )
 def test_backward_rejects_degenerate_strides(over, msg):
     assert _bwd_call(**over) == _lib.HARP_RA_EINVAL
     assert msg in _lib.last_error()
+
+
+@pytest.mark.parametrize("dkt", [_lib.HARP_RA_BF16, _lib.HARP_RA_F32])
+def test_backward_unaligned_dkdv_views_pass_validation_below_head_dim_128(dkt):
+    """The dK / dV kernel for head dims other than 128 stores element by
+    element, so bf16 (and fp32) dK / dV views at an odd element offset with
+    an odd row stride are accepted there: validation gets past them to the
+    statistics check (m_i NULL here, so nothing is launched)."""
+    odd = _lib.i64_array([8 * 65 * 128, 65, 8 * 65, 1])
+    rc = _bwd_call(dkc=_lib.ptr_array([(1 << 20) + 2]), dvc=_lib.ptr_array([(1 << 21) + 2]), dks=odd, dkt=dkt,
+                   m=None)
+    assert rc == _lib.HARP_RA_EINVAL
+    assert "m_i / l_i / delta are NULL" in _lib.last_error()
 
 
 def _cpu_qkv(T=16, Tk=16, H=2, D=64):
