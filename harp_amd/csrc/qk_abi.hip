@@ -98,18 +98,23 @@ size_t bwd_ws_bytes(const QkShape& sh) { return bwd_workspace_floats(sh) * sizeo
 // one buffer per (device, stream): calls on one stream run in order and so
 // never overlap on their buffer, and calls on different streams never share
 // one.  A buffer that must grow is freed only after its stream has drained
-// (earlier calls may still read it).  This path calls hipMalloc / hipFree, so
-// it cannot be captured into a HIP graph; callers that capture pass their own
-// workspace.
+// (earlier calls may still read it).  At most kMaxOwned buffers are kept: a
+// call on a new stream when the table is full frees the least recently used
+// buffer first, after waiting for its whole device (its stream may no longer
+// exist).  This path calls hipMalloc / hipFree, so it cannot be captured into
+// a HIP graph; callers that capture pass their own workspace.
+constexpr size_t kMaxOwned = 8;
 struct OwnedWorkspace {
   struct Buf {
     int dev;
     hipStream_t stream;
     void* ptr;
     size_t bytes;
+    uint64_t last_use;
   };
   std::mutex mu;
   std::vector<Buf> bufs;
+  uint64_t clock = 0;
 };
 OwnedWorkspace& owned() {
   static OwnedWorkspace w;
@@ -130,9 +135,24 @@ int resolve_workspace(void** ws, size_t* ws_bytes, size_t need, hipStream_t stre
   for (auto& x : w.bufs)
     if (x.dev == dev && x.stream == stream) b = &x;
   if (!b) {
-    w.bufs.push_back(OwnedWorkspace::Buf{dev, stream, nullptr, 0});
+    if (w.bufs.size() >= kMaxOwned) {
+      size_t lru = 0;
+      for (size_t i = 1; i < w.bufs.size(); ++i)
+        if (w.bufs[i].last_use < w.bufs[lru].last_use) lru = i;
+      OwnedWorkspace::Buf& e = w.bufs[lru];
+      if (e.ptr) {
+        if (e.dev != dev && hipSetDevice(e.dev) != hipSuccess) return fail(HARP_QK_ELAUNCH, "hipSetDevice failed");
+        const bool synced = hipDeviceSynchronize() == hipSuccess;
+        if (synced) (void)hipFree(e.ptr);
+        if (e.dev != dev && hipSetDevice(dev) != hipSuccess) return fail(HARP_QK_ELAUNCH, "hipSetDevice failed");
+        if (!synced) return fail(HARP_QK_ELAUNCH, "hipDeviceSynchronize failed");
+      }
+      w.bufs.erase(w.bufs.begin() + (std::ptrdiff_t)lru);
+    }
+    w.bufs.push_back(OwnedWorkspace::Buf{dev, stream, nullptr, 0, 0});
     b = &w.bufs.back();
   }
+  b->last_use = ++w.clock;
   if (b->bytes < need) {
     if (b->ptr) {
       if (hipStreamSynchronize(stream) != hipSuccess) return fail(HARP_QK_ELAUNCH, "hipStreamSynchronize failed");

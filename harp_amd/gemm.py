@@ -136,14 +136,17 @@ def xhblas_gemm(order: int, trans_a: int, trans_b: int, M: int, N: int, K: int, 
         return -3
     if M < 0 or N < 0 or K < 0:
         return -4
-    if M == 0 or N == 0:
-        return 0
-    if beta != 0.0:
-        return -8
+    # the reference's order (bgemm.cpp:324-349): leading dimensions before
+    # beta; it returns -6 for a shape outside its table, where every shape
+    # runs here
     a_cols = K if trans_a == NO_TRANS else M
     b_cols = N if trans_b == NO_TRANS else K
     if lda != a_cols or ldb != b_cols or ldc != N:
         return -5
+    if beta != 0.0:
+        return -8
+    if M == 0 or N == 0:
+        return 0
     for name, t in (("A", A), ("B", B), ("C", C)):
         if not t.is_cuda:
             raise RuntimeError(f"xhblas_gemm: {name} must be on a HIP device (there is no CPU path)")

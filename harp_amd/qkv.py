@@ -50,13 +50,26 @@ def _freqs_table(freqs_cis: torch.Tensor, B: int, S: int) -> Tuple[torch.Tensor,
     return r, sb, r.stride(-2)
 
 
+MAX_LD = 1 << 22  # harp_qkv_project: a 256-row tile of x or W spans < 2^32 bytes
+
+
+def _aligned16(t: torch.Tensor) -> bool:
+    return t.data_ptr() % 16 == 0
+
+
 def fused_supported(attn, hidden_states: torch.Tensor, freqs_cis: Optional[torch.Tensor]) -> bool:
-    """True when :func:`qkv_project` takes this attention module and input."""
+    """True when :func:`qkv_project` takes this attention module and input:
+    the checks harp_qkv_project makes (shapes, dtypes, leading dimensions
+    multiples of 8 up to 2^22, 16-byte aligned x / weight / norm-weight /
+    RoPE-table pointers), made on what qkv_project would pass it, so that
+    anything the kernel refuses takes the unfused path instead of raising."""
     x = hidden_states
     if not (x.is_cuda and x.dtype == torch.bfloat16 and x.dim() == 3 and x.stride(-1) == 1):
         return False
     K = x.size(-1)
-    if K % K_TILE or K == 0:
+    if K % K_TILE or K == 0 or K > MAX_LD:
+        return False
+    if x.is_contiguous() and not _aligned16(x):  # qkv_project passes x itself (a copy only when strided)
         return False
     lins = [getattr(attn, n, None) for n in ("to_q", "to_k", "to_v")]
     if any(m is None or getattr(m, "bias", None) is not None or not hasattr(m, "weight") for m in lins):
@@ -68,6 +81,8 @@ def fused_supported(attn, hidden_states: torch.Tensor, freqs_cis: Optional[torch
         w = m.weight
         if w.dtype != torch.bfloat16 or w.device != x.device or tuple(w.shape) != (n_out, K) or w.stride(-1) != 1:
             return False
+        if w.stride(0) % 8 or not K <= w.stride(0) <= MAX_LD or not _aligned16(w):
+            return False
     norms = [getattr(attn, "norm_q", None), getattr(attn, "norm_k", None)]
     for nm in norms:
         if nm is None:
@@ -75,12 +90,16 @@ def fused_supported(attn, hidden_states: torch.Tensor, freqs_cis: Optional[torch
         w = getattr(nm, "weight", None)
         if w is None or w.dtype not in (torch.bfloat16, torch.float32) or w.device != x.device or w.numel() != HEAD_DIM:
             return False
+        if not w.is_contiguous() or not _aligned16(w):
+            return False
     if freqs_cis is not None:
         if any(nm is None for nm in norms) or not freqs_cis.is_cuda or freqs_cis.device != x.device:
             return False  # RoPE without RMSNorm runs on the separate operator
         try:
-            _freqs_table(freqs_cis, x.size(0), x.size(1))
+            table, _, _ = _freqs_table(freqs_cis, x.size(0), x.size(1))
         except ValueError:
+            return False
+        if not _aligned16(table):
             return False
     return x.size(0) * x.size(1) < (1 << 31)
 

@@ -70,7 +70,9 @@ HARP_QK_API int harp_qk_rmsnorm_forward(const void* x, const int64_t* x_strides,
  * one such buffer per (device, stream), grown with hipMalloc when a call needs
  * more (after the stream drains): calls on different streams never share it,
  * but a NULL-workspace call allocates and so cannot be captured into a HIP
- * graph; callers that capture pass a workspace.
+ * graph; callers that capture pass a workspace.  At most 8 such buffers are
+ * kept until the process ends: a NULL-workspace call on a ninth stream first
+ * frees the least recently used one, after a device-wide synchronisation.
  * Replaces: rmsnorm_backward_out(Tensor input, Tensor grad_output, Tensor
  *   weight, Tensor rms, Tensor(a!) grad_input, Tensor(b!) grad_weight) —
  *   async_rt/csrc/rms_norm.cc:484-522 (kernel :107-240), schema

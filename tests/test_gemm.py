@@ -21,11 +21,17 @@ DUMMY = torch.zeros(1, dtype=torch.bfloat16)  # never touched: validation return
         (dict(trans_b=7), -3),
         (dict(M=-1), -4),
         (dict(M=0), 0),  # nothing to do
-        (dict(N=0), 0),
+        (dict(N=0, ldb=0, ldc=0), 0),
         (dict(beta=1.0), -8),
         (dict(lda=65), -5),
         (dict(ldb=17), -5),
         (dict(ldc=31), -5),
+        # bgemm.cpp:324-349 checks the leading dimensions before beta and
+        # before anything is done, degenerate sizes included
+        (dict(M=0, lda=65), -5),
+        (dict(N=0, ldc=31), -5),
+        (dict(lda=65, beta=1.0), -5),
+        (dict(M=0, beta=1.0), -8),
     ],
 )
 def test_status_codes_match_the_reference(args, code):

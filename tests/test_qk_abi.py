@@ -200,3 +200,75 @@ def test_qkv_project_validates_shapes_before_the_kernel():
     w = torch.zeros((256, 128), dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="HIP device"):
         qkv.qkv_project(x, [w, w, w], [(None, 0.0)] * 3, None)
+
+
+class _DevView:
+    """A CPU tensor that answers as a device tensor at a chosen address, so
+    fused_supported's pointer and stride checks run without a GPU."""
+
+    is_cuda = True
+    device = "cuda:0"
+
+    def __init__(self, t, addr=1 << 20):
+        self.t, self.addr = t, addr
+
+    dtype = property(lambda self: self.t.dtype)
+    shape = property(lambda self: self.t.shape)
+
+    def dim(self):
+        return self.t.dim()
+
+    def size(self, *a):
+        return self.t.size(*a)
+
+    def stride(self, *a):
+        return self.t.stride(*a)
+
+    def numel(self):
+        return self.t.numel()
+
+    def is_contiguous(self):
+        return self.t.is_contiguous()
+
+    def data_ptr(self):
+        return self.addr
+
+
+def _module(K=128, H=2, wq=None, nw=None):
+    from types import SimpleNamespace
+
+    n = H * 128
+    lin = [SimpleNamespace(weight=_DevView(torch.zeros(n, K, dtype=torch.bfloat16)), bias=None) for _ in range(3)]
+    if wq is not None:
+        lin[0].weight = wq
+    norm = SimpleNamespace(weight=nw if nw is not None else _DevView(torch.ones(128, dtype=torch.bfloat16)), eps=1e-6)
+    return SimpleNamespace(heads=H, to_q=lin[0], to_k=lin[1], to_v=lin[2], norm_q=norm, norm_k=norm)
+
+
+def test_fused_supported_mirrors_the_kernel_checks():
+    """Everything harp_qkv_project refuses (weight leading dimension not a
+    multiple of 8 or above 2^22, misaligned x / weight / norm weight, a
+    strided norm weight) takes the unfused path instead of raising."""
+    from harp_amd import qkv
+
+    x = _DevView(torch.zeros(1, 16, 128, dtype=torch.bfloat16))
+    assert qkv.fused_supported(_module(), x, None)
+    # a misaligned hidden-state slice (contiguous: passed as is)
+    assert not qkv.fused_supported(_module(), _DevView(x.t, (1 << 20) + 2), None)
+    # a weight at an address that is not 16-byte aligned
+    assert not qkv.fused_supported(_module(wq=_DevView(torch.zeros(256, 128, dtype=torch.bfloat16), (1 << 20) + 4)),
+                                   x, None)
+    # weight rows padded to a stride that is not a multiple of 8
+    odd = torch.zeros(256, 131, dtype=torch.bfloat16)[:, :128]
+    assert odd.stride(0) == 131
+    assert not qkv.fused_supported(_module(wq=_DevView(odd)), x, None)
+    ok8 = torch.zeros(256, 136, dtype=torch.bfloat16)[:, :128]
+    assert qkv.fused_supported(_module(wq=_DevView(ok8)), x, None)
+    # leading dimension above 2^22 elements
+    huge = _DevView(torch.zeros(256, 128, dtype=torch.bfloat16))
+    huge.stride = lambda *a: ((1 << 22) + 8, 1)[a[0]] if a else ((1 << 22) + 8, 1)
+    assert not qkv.fused_supported(_module(wq=huge), x, None)
+    # norm weight: misaligned, or a strided view
+    assert not qkv.fused_supported(_module(nw=_DevView(torch.ones(128, dtype=torch.bfloat16), (1 << 20) + 2)), x,
+                                   None)
+    assert not qkv.fused_supported(_module(nw=_DevView(torch.ones(256, dtype=torch.bfloat16)[::2])), x, None)
