@@ -513,18 +513,19 @@ class Workload:
 
     def timed(self, steps: int, warmup: int) -> dict:
         """warmup untimed steps, then `steps` timed ones (HIP events on the
-        current stream, one per step) with the library's per-kernel launch
-        timing on; returns ms per step (mean and median), per-kernel (ms,
-        launches) and the host wall time of the timed region."""
+        current stream, one per step, nothing else recorded in between: the
+        step time is the operators' own), then `steps` more with the
+        library's per-kernel launch timing on (its event pairs around every
+        launch add gaps to the stream, so those steps only give the per-kernel
+        breakdown).  Returns ms per step (mean and median of the first timed
+        steps), per-kernel (ms, launches) of the second, and the host wall
+        time of the first."""
         import torch
 
         from harp_amd import _lib
 
         for _ in range(warmup):
             self.step()
-        torch.cuda.synchronize()
-        _lib.timing_read()  # discard
-        _lib.timing_enable(True)
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
         torch.cuda.synchronize()
         t_wall = time.perf_counter()
@@ -534,11 +535,16 @@ class Workload:
             ev[i + 1].record()
         torch.cuda.synchronize()
         wall_s = time.perf_counter() - t_wall
-        _lib.timing_enable(False)
-        kt = _lib.timing_read()
         step_ms = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(steps))
         med = step_ms[len(step_ms) // 2] if len(step_ms) % 2 else 0.5 * (
             step_ms[len(step_ms) // 2 - 1] + step_ms[len(step_ms) // 2])
+        _lib.timing_read()  # discard
+        _lib.timing_enable(True)
+        for _ in range(steps):
+            self.step()
+        torch.cuda.synchronize()
+        _lib.timing_enable(False)
+        kt = _lib.timing_read()
         return {"ms": ev[0].elapsed_time(ev[-1]) / steps, "median_ms": med, "kernels": kt, "wall_s": wall_s}
 
 
