@@ -306,6 +306,38 @@ def producer_bench(cfg, seed: int, iters: int = 20):
         "norm_rope_q_and_k_bytes": int(2 * fwd_bytes),
         "norm_rope_q_and_k_frac_hbm_peak": round(2 * fwd_bytes / (ms_nr * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
     }
+
+    # The producer's backward as training runs it (ProjectQKVFn): the fused
+    # RMSNorm + RoPE backward of q and k, then dX (three GEMMs into one
+    # accumulator) and dW (three GEMMs); gradients of all inputs, none
+    # accumulated into .grad.
+    hid_g = hid.clone().requires_grad_(True)
+    wts = [m.weight.detach().clone().requires_grad_(True) for m in lin]
+    nw_g = w.detach().clone().requires_grad_(True)
+    q_o, k_o, v_o = _qkv.ProjectQKVFn.apply(hid_g, wts[0], wts[1], wts[2], nw_g, nw_g, freqs, 1e-6, 1e-6)
+    grads = [torch.randn(t.shape, generator=g).to(torch.bfloat16).to(dev).as_strided(t.shape, t.stride())
+             for t in (q_o, k_o, v_o)]
+    ins = [hid_g, *wts, nw_g]
+    ms_b = timed(lambda: torch.autograd.grad([q_o, k_o, v_o], ins, grads, retain_graph=True), n=iters, warm=5)
+    gq = torch.empty((B, T, dim), device=dev, dtype=torch.bfloat16)
+    gq4 = gq.unflatten(-1, (H, D)).transpose(1, 2)
+    lin4 = torch.randn((B, T, dim), generator=g).to(torch.bfloat16).to(dev).unflatten(-1, (H, D)).transpose(1, 2)
+    gwt = torch.empty(D, device=dev, dtype=torch.bfloat16)
+    with torch.no_grad():
+        ms_nrb = timed(lambda: (ops.qk_norm_rope_backward(lin4, grads[0], w, rms_q, freqs, gq4, gwt),
+                                ops.qk_norm_rope_backward(lin4, grads[1], w, rms_q, freqs, gq4, gwt)))
+    bwd_flop = 2 * gemm_flop  # dX and dW: each the forward's three products
+    res["project_qkv_backward"] = {
+        "avg_ms": round(ms_b, 4),
+        "gemm_flop": bwd_flop,
+        "tflops_gemms": round(bwd_flop / (ms_b * 1e-3) / 1e12, 1),
+        "norm_rope_backward_q_and_k_ms": round(ms_nrb, 4),
+        "norm_rope_backward_q_and_k_bytes": int(2 * bwd_bytes),
+        "norm_rope_backward_q_and_k_frac_hbm_peak": round(2 * bwd_bytes / (ms_nrb * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+        "what": "ProjectQKVFn backward through autograd: fused RMSNorm + RoPE backward of q and k "
+                "(async_op.qk_norm_rope_backward), then dX = sum of three products and dW of each weight "
+                "(hipBLASLt); gradients of hidden, the three weights and the norm weight",
+    }
     return res
 
 
