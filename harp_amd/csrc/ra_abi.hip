@@ -489,6 +489,16 @@ int harp_ra_backward(const void* q, const int64_t* q_strides, void* grad_q, cons
   if ((rc = check_bf16_view(grad_out, do_strides, h_len, "grad_out"))) return rc;
   if ((rc = check_out_view(grad_q, dq_strides, batch, h_num, t_num, h_len, "grad_q"))) return rc;
   if (dq_dtype != HARP_RA_F32 && dq_dtype != HARP_RA_BF16) return fail(HARP_RA_EINVAL, "dq_dtype must be F32 or BF16");
+  // at head dim 128 the dQ kernel stores bf16 rows four elements (8 bytes)
+  // per lane store too
+  if (dq_dtype == HARP_RA_BF16 && h_len == 128) {
+    for (int i = 0; i < 3; ++i)
+      if (dq_strides[i] % 4 != 0)
+        return fail(HARP_RA_EINVAL, "bf16 grad_q stride[%d]=%lld must be a multiple of 4 elements at h_len 128", i,
+                    (long long)dq_strides[i]);
+    if ((reinterpret_cast<uintptr_t>(grad_q) & 7u) != 0)
+      return fail(HARP_RA_EINVAL, "bf16 grad_q must be 8-byte aligned at h_len 128");
+  }
   if (dkv_dtype != HARP_RA_F32 && dkv_dtype != HARP_RA_BF16)
     return fail(HARP_RA_EINVAL, "dkv_dtype must be F32 or BF16");
   if (!k_chunks || !v_chunks || !dk_chunks || !dv_chunks) return fail(HARP_RA_EINVAL, "chunk pointer arrays are NULL");

@@ -981,34 +981,60 @@ __global__ __launch_bounds__(64 * kDkWaves, 1) void dkdv_kernel(BwdParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// KV-split merges: 16 lanes per query row, 8 elements of D per lane
+// KV-split merges: 16 lanes per query row, 8 elements of D per lane.  The
+// splits are read kMergeGroup at a time, all loads of a group issued before
+// any is used (an index past the last split reads the last one again and is
+// given no weight), so a merge of n splits waits for ceil(n / 8) load
+// latencies instead of n.
 // ---------------------------------------------------------------------------
+constexpr int kMergeGroup = 8;
+
 __global__ __launch_bounds__(256) void fwd_merge_kernel(FwdMergeParams p) {
   const int64_t rows = (int64_t)p.B * p.H * p.T;
   const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
   const int sub = threadIdx.x & 15, d0 = sub * 8;
   if (row >= rows) return;  // whole 16-lane groups
+  const bool has_d = d0 < p.D;
+  const int dr = has_d ? d0 : 0;  // lanes past D read (and drop) elements 0..7
   float mx = -INFINITY;
-  for (int s = 0; s < p.n_split; ++s) mx = fmaxf(mx, p.part_m[s * rows + row]);
+  for (int s0 = 0; s0 < p.n_split; s0 += kMergeGroup) {
+    float ms[kMergeGroup];
+#pragma unroll
+    for (int u = 0; u < kMergeGroup; ++u) ms[u] = p.part_m[min(s0 + u, p.n_split - 1) * rows + row];
+#pragma unroll
+    for (int u = 0; u < kMergeGroup; ++u) mx = fmaxf(mx, ms[u]);  // a repeated split changes no maximum
+  }
   float l = 0.f, acc[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) acc[j] = 0.f;
-  for (int s = 0; s < p.n_split; ++s) {
-    const float ls = p.part_l[s * rows + row];
-    // a split without keys (l = 0) adds nothing; NaN statistics propagate
-    const float w = (ls == 0.f) ? 0.f : ls * __expf(p.part_m[s * rows + row] - mx);
-    l += w;
-    if (w != 0.f && d0 < p.D) {
-      const float* o = p.part_o + (s * rows + row) * p.D + d0;
+  for (int s0 = 0; s0 < p.n_split; s0 += kMergeGroup) {
+    float ms[kMergeGroup], ls[kMergeGroup], o[kMergeGroup][8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc[j] += w * o[j];
+    for (int u = 0; u < kMergeGroup; ++u) {
+      const int64_t sr = min(s0 + u, p.n_split - 1) * rows + row;
+      ms[u] = p.part_m[sr];
+      ls[u] = p.part_l[sr];
+      const float* op = p.part_o + sr * p.D + dr;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[u][j] = op[j];
+    }
+#pragma unroll
+    for (int u = 0; u < kMergeGroup; ++u) {
+      if (s0 + u >= p.n_split) break;
+      // a split without keys (l = 0) adds nothing; NaN statistics propagate
+      const float w = (ls[u] == 0.f) ? 0.f : ls[u] * __expf(ms[u] - mx);
+      l += w;
+      if (w != 0.f) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] += w * o[u][j];
+      }
     }
   }
   const int t = (int)(row % p.T);
   const int64_t bh = row / p.T;
   const int h = (int)(bh % p.H), b = (int)(bh / p.H);
   const float inv = (l > 0.f) ? 1.f / l : 0.f;
-  if (d0 < p.D) {
+  if (has_d) {
     float* orow = p.out + (int64_t)b * p.sob + (int64_t)h * p.soh + (int64_t)t * p.sot + d0;
 #pragma unroll
     for (int j = 0; j < 8; ++j) orow[j] = acc[j] * inv;
@@ -1034,10 +1060,20 @@ __global__ __launch_bounds__(256) void dq_merge_kernel(DqMergeParams p) {
   float acc[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) acc[j] = 0.f;
-  for (int s = 0; s < p.n_split; ++s) {
-    const float* o = p.part + (s * rows + row) * p.D + d0;
+  for (int s0 = 0; s0 < p.n_split; s0 += kMergeGroup) {
+    float o[kMergeGroup][8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc[j] += o[j];
+    for (int u = 0; u < kMergeGroup; ++u) {
+      const float* op = p.part + (min(s0 + u, p.n_split - 1) * rows + row) * p.D + d0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[u][j] = op[j];
+    }
+#pragma unroll
+    for (int u = 0; u < kMergeGroup; ++u) {
+      if (s0 + u >= p.n_split) break;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] += o[u][j];
+    }
   }
   const int t = (int)(row % p.T);
   const int64_t bh = row / p.T;

@@ -87,10 +87,11 @@ HARP_RA_API int harp_ra_forward(const void* q, const int64_t* q_strides,
  * (256-byte aligned), or NULL to use a grow-only per-device buffer owned by
  * the library (calls with a NULL workspace that overlap on one device then
  * race; that path may call hipMalloc, so graph-captured calls pass one).
- * bf16 dK / dV at h_len 128 are stored 8 bytes per lane: every dK / dV chunk
- * pointer must then be 8-byte aligned and every dkv_strides entry a multiple
- * of 4 elements (HARP_RA_EINVAL otherwise).  fp32 dK / dV, and bf16 at other
- * head dims, only need the view rules of the other outputs.
+ * bf16 dQ, dK and dV at h_len 128 are stored 8 bytes per lane: grad_q and
+ * every dK / dV chunk pointer must then be 8-byte aligned and every
+ * dq_strides / dkv_strides entry a multiple of 4 elements (HARP_RA_EINVAL
+ * otherwise).  fp32 gradients, and bf16 at other head dims, only need the
+ * view rules of the other outputs.
  */
 HARP_RA_API int harp_ra_backward(const void* q, const int64_t* q_strides,
                      void* grad_q, const int64_t* dq_strides, int dq_dtype,

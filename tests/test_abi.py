@@ -179,6 +179,11 @@ def _bwd_call(**over):
               dks=_lib.i64_array([8 * 130 * 128, 130, 8 * 130, 1])), "must be a multiple of 4 elements"),
         (dict(D=128, qs=_ST128, dqs=_ST128, ks=_ST128, dos=_ST128, dks=_ST128,
               dkc=_lib.ptr_array([(1 << 20) + 2])), "must be 8-byte aligned"),
+        # and so are bf16 dQ rows
+        (dict(D=128, qs=_ST128, ks=_ST128, dos=_ST128, dks=_ST128,
+              dqs=_lib.i64_array([8 * 130 * 128, 130, 8 * 130, 1])), "grad_q stride[1]=130 must be a multiple"),
+        (dict(D=128, qs=_ST128, dqs=_ST128, ks=_ST128, dos=_ST128, dks=_ST128, dq=(1 << 20) + 2),
+         "bf16 grad_q must be 8-byte aligned"),
     ],
 )
 def test_backward_rejects_degenerate_strides(over, msg):
