@@ -19,18 +19,19 @@ Slot J (one per key block):
          S(J+1)  = K(J+1) Q^T          (16 MFMAs, Q in a128..a191)
   VALU   online softmax of S(J): P(J) = bf16 of exp2(S c2 - m_ref) against
          the lane's current reference point m_ref, row sums (fp32, unrounded
-         exps), the lane's running maximum of the raw scores, and the rescale
-         check: a lane whose 16 exps of the block sum above 2^8 (some key
-         above m_ref + 8 in log2 units, or the first keys of a row, whose
-         m_ref is still -FLT_MAX and whose exps overflow) flags the wave
+         exps), and the rescale check: a lane whose 16 exps of the block sum
+         above 2^8 (some key above m_ref + 8 in log2 units, or the first keys
+         of a row, whose m_ref is still -FLT_MAX and whose exps overflow)
+         flags the wave
   copies of block J + 5 (4 per wave)
 The loop is unrolled over the eight buffers; each slot has a masked twin
 (keys past a chunk's valid length set to -inf) entered when its block is a
 chunk's partial last one, and an out-of-line rescale (one per slot parity):
-m_ref moves to the row's running maximum (both lane halves), O and l are
-multiplied by 2^(old - new), and P(J) and the block sums are computed again
-from S(J), which the exps leave intact.  The exact row maximum is the lanes'
-running maxima, combined once by the kernel's epilogue.
+m_ref moves up to the row's maximum over block J (both lane halves), O and l
+are multiplied by 2^(old - new), and P(J) and the block sums are computed
+again from S(J), which the exps leave intact.  The kernel writes m_ref as the
+row statistic m, with l relative to it: m + log l is the row's LSE (what the
+backward reads); m is within 8 log2 units below the row's exact maximum.
 The reference math is ring_attn.cpp:2412-2575 (ring_attention_forward).
 """
 import os
@@ -41,7 +42,7 @@ from asm_sched import Emitter, clobber_list, fill_schedule, ins, regs_of  # noqa
 
 # ---- registers ------------------------------------------------------------
 KADDR, VADDR, DOFF = 32, 40, 48          # per-lane LDS addresses / copy offsets
-MREF, MMAX, LRUN, LSUM, MNEW, MX = 50, 52, 54, 56, 58, 60  # pairs (qg)
+MREF, MMAX, LRUN, LSUM, MNEW, MX = 50, 52, 54, 56, 58, 60  # pairs (qg); MMAX unused
 KF, VF = 64, 80                          # 4 fragment buffers x 4 registers each
 P = (96, 112)                            # P[par]: qg * 8 + k2 * 4 + w
 S = (128, 160)                           # S[par]: qg * 16 + r
@@ -182,17 +183,7 @@ def softmax(par, masked):
             for qg in range(2):
                 L.append(ins(f"v_cndmask_b32_e32 {sv(qg, r)}, {sv(qg, r)}, {v(NEGV)}, vcc", "valu", dst=sv(qg, r),
                              src=[*[sv(qg, r)], v(NEGV), "vcc"]))
-    body = exp_pipeline(par)
-    # the lane's running maximum of the raw scores, between the pipeline's first instructions
-    mx = []
-    for step in range(8):
-        for qg in range(2):
-            m = v(MMAX + qg)
-            mx.append(ins(f"v_max3_f32 {m}, {m}, {sv(qg, 2 * step)}, {sv(qg, 2 * step + 1)}", "valu", dst=m,
-                          src=f"{m} {sv(qg, 2 * step)} {sv(qg, 2 * step + 1)}"))
-    for i, x in enumerate(mx):
-        body.insert(8 + 5 * i, x)
-    L += body
+    L += exp_pipeline(par)
     for qg in range(2):  # a block sum above 2^8 (or inf) flags the wave for the rescale; NaN does not
         L.append(ins(f"v_cmp_lt_f32_e32 vcc, {LIMIT}, {v(LSUM + qg)}", "valu", dst=["vcc"], src=v(LSUM + qg)))
         L.append(ins(f"s_or_b64 {s(FLAG, 2)}, {s(FLAG, 2)}, vcc", "salu", dst=s(FLAG, 2),
@@ -326,16 +317,24 @@ def prologue():
 
 
 def rescale(par):
-    """After slot J (parity par) flagged: m_ref moves to c2 times the row's
-    running maximum over both lane halves (at least -FLT_MAX), O and l are
-    multiplied by corr = 2^(m_ref - m_new) (m_new >= m_ref: 1 where
+    """After slot J (parity par) flagged: m_ref moves to the larger of itself
+    and c2 times the row's maximum over block J (both lane halves), O and l
+    are multiplied by corr = 2^(m_ref - m_new) (m_new >= m_ref: 1 where
     unchanged, 0 from -FLT_MAX), and P(J) and the block sums are computed
-    again against the new reference from S(J)."""
+    again against the new reference from S(J).  Blocks that did not flag
+    have every exp at most 2^8 (their sums are), so every score seen so far
+    stays within 8 (log2 units) above the new m_ref."""
     em = Emitter()
     em.nop(16)  # the last O MFMAs of the slot
     m0, m1 = v(MX), v(MX + 1)
-    for qg in range(2):
-        em.emit(ins(f"v_mov_b32_e32 {v(MX + qg)}, {v(MMAX + qg)}", "valu", dst=v(MX + qg), src=v(MMAX + qg)))
+    cur = S[par]
+    for qg in range(2):  # the lane's maximum of block J's raw scores (masked keys are -inf)
+        sv = lambda r: v(cur + 16 * qg + r)
+        mx = v(MX + qg)
+        em.emit(ins(f"v_max_f32_e32 {mx}, {sv(0)}, {sv(1)}", "valu", dst=mx, src=f"{sv(0)} {sv(1)}"))
+        for r in range(2, 16, 2):
+            em.emit(ins(f"v_max3_f32 {mx}, {mx}, {sv(r)}, {sv(r + 1)}", "valu", dst=mx,
+                        src=f"{mx} {sv(r)} {sv(r + 1)}"))
     # [mx0 lo | mx0 hi], [mx1 lo | mx1 hi] -> swap, max -> [M0 | M1] -> copy, swap -> [M0 | M0], [M1 | M1]
     em.emit(ins(f"v_permlane32_swap_b32_e32 {m0}, {m1}", "perm", dst=f"{m0} {m1}", src=f"{m0} {m1}"))
     em.emit(ins(f"v_max_f32_e32 {m0}, {m0}, {m1}", "valu", dst=m0, src=f"{m0} {m1}"))
@@ -344,7 +343,7 @@ def rescale(par):
     for qg in range(2):
         mn, t, c = v(MNEW + qg), v(TMP + qg), v(CORR + qg)
         em.emit(ins(f"v_mul_f32_e32 {mn}, %[c2], {v(MX + qg)}", "valu", dst=mn, src=v(MX + qg)))
-        em.emit(ins(f"v_max_f32_e32 {mn}, {NEG_BIG}, {mn}", "valu", dst=mn, src=mn))
+        em.emit(ins(f"v_max_f32_e32 {mn}, {v(MREF + qg)}, {mn}", "valu", dst=mn, src=f"{v(MREF + qg)} {mn}"))
         em.emit(ins(f"v_sub_f32_e32 {t}, {v(MREF + qg)}, {mn}", "valu", dst=t, src=f"{v(MREF + qg)} {mn}"))
         em.emit(ins(f"v_exp_f32_e32 {c}, {t}", "trans", dst=c, src=t))
     for qg in range(2):

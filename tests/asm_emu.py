@@ -706,7 +706,9 @@ def run_dq_block(q, do, ks, vs, lens, order, stats0, stats1, scale, lines=None):
 
 def run_fwd_block(q, ks, vs, lens, order, scale, lines=None):
     """forward of query rows 0..255 over the chunks: O [T, 128], m (natural
-    log units, the exact row max of the scaled scores) and l (relative to m)."""
+    log units: the loop's reference point, within 8 log2 units below the row
+    max of the scaled scores; -inf for a row without keys) and l (relative
+    to m)."""
     T = q.shape[0]
     mem = Mem()
     ops0 = _chunk_setup(mem, ks, vs, lens, order)
@@ -721,7 +723,7 @@ def run_fwd_block(q, ks, vs, lens, order, scale, lines=None):
         _row_addrs(mv)
         _tr_addrs(mv, 8, 65536)
         _copy_offs(mv, 16, w)
-        for i in (18, 19, 20, 21, 26, 27):
+        for i in (18, 19, 26, 27):
             mv[i] = ninf
         wv.v[32:64] = mv.astype(np.uint32)
         m2 = np.zeros((32, 64), dtype=np.uint32)
@@ -740,20 +742,18 @@ def run_fwd_block(q, ks, vs, lens, order, scale, lines=None):
         af = waves[w].a.view(np.float32)
         for qg in range(2):
             m_ref, l = vf[50 + qg], vf[54 + qg]
-            m_max = c2 * np.maximum(vf[52 + qg], np.roll(vf[52 + qg], 32))  # lanes' running raw maxima
             l_tot = l + np.roll(l, 32)
             for ln in range(64):
                 qi = w * 64 + qg * 32 + (ln & 31)
                 if qi >= T:
                     continue
-                shift = 1.0 if m_max[ln] == -np.inf else 2.0 ** (float(m_ref[ln]) - float(m_max[ln]))
                 inv = 1.0 / l_tot[ln] if l_tot[ln] > 0 else 0.0
                 for db in range(4):
                     for r in range(16):
                         d = db * 32 + 8 * (r // 4) + 4 * (ln >> 5) + r % 4
                         O[qi, d] = af[64 * qg + 16 * db + r, ln] * inv
-                m_out[qi] = float(m_max[ln]) * np.log(2.0)
-                l_out[qi] = float(l_tot[ln]) * shift
+                m_out[qi] = float(m_ref[ln]) * np.log(2.0) if l_tot[ln] > 0 else -np.inf
+                l_out[qi] = float(l_tot[ln])
     return O, m_out, l_out
 
 

@@ -108,7 +108,8 @@ def test_dq_and_fwd_every_loop_exit(nb, ragged):
     Of, mf, lf = emu.run_fwd_block(q, ks, vs, [n], [0], scale)
     assert _rel(Of, O) < 1e-2
     assert np.abs(mf + np.log(lf) - lse_r).max() < 1e-4
-    assert np.abs(mf - m_r).max() < 1e-4  # m is the exact row max
+    # m is the exps' reference point: at most 8 log2 units below the row max
+    assert (mf <= m_r + 1e-4).all() and (mf >= m_r - 8 * np.log(2.0) - 1e-4).all()
 
 
 @pytest.mark.parametrize("rank", [0, 2, 4])
