@@ -69,6 +69,10 @@ def _inputs(B, H, T, D, N, tc, vscale, seed=3407):
     (3, 2, 16, 4096, 72, 8, 4096, None, 0.5),
     (4, 1, 24, 8192, 128, 8, 8192, None, 1.0),
     (5, 1, 24, 4429, 128, 4, 4480, [4429] * 4, 1.0),
+    # HARP's own call shapes (30 heads of 128, 256 / 768 local rows, 8 ring
+    # steps): eight- and two-way KV splits of the forward and dQ kernels
+    ("harp-256", 1, 30, 256, 128, 8, 256, None, 1.0),
+    ("harp-768", 1, 30, 768, 128, 8, 768, None, 1.0),
 ])
 def test_full_size_against_fp32_reference(config, B, H, T, D, N, tc, lens, vscale):
     print(f"[config {config} full size]", flush=True)
