@@ -22,6 +22,7 @@
 // are issued two steps ahead of the MFMAs that consume them.
 // Accumulation is fp32 in registers; P and dS are rounded to bf16 only as
 // MFMA operands; exp is v_exp_f32 (exp2) with log2(e) folded into the scale.
+#include "cq_epilogue.h"
 #include "ra_common.h"
 #include "ra_kernels.h"
 
@@ -472,16 +473,50 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
   // across the loop for them)
   const int lane_e = lane_id_fresh(), g_e = lane_e >> 5;
   const int qi_e = qt * kFwdRows + wave * 32 + (lane_e & 31);
-  if (qi_e >= p.T) return;
-  float* orow = p.out + sp.index * p.split_o + (int64_t)b * p.sob + (int64_t)h * p.soh + (int64_t)qi_e * p.sot;
+  using E = cq_epi::QRows<DP>;
+  if constexpr (E::kHalfBytes <= (int)sizeof(Ks) && E::kHalfBytes <= (int)sizeof(Vs)) {
+    // O / l staged through LDS (cq_epilogue.h: waves 0-3 in the K tiles,
+    // 4-7 in the V tiles), then every query row stored as contiguous
+    // 16-byte pieces instead of one element per lane and store
+    float* const st = (float*)(cq_epi::half(wave) ? &Vs[0][0][0] : &Ks[0][0][0]) + E::stage_base(wave);
+    __syncthreads();  // every wave is done with the loop's K / V tiles
 #pragma unroll
-  for (int db = 0; db < DBLK; ++db)
+    for (int db = 0; db < DBLK; ++db)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int d = db * 32 + c_row(r, g_e);
-      if (d < p.D) orow[d] = o[db][r] * inv;
+      for (int i = 0; i < 4; ++i) {
+        const f32x4 x = {o[db][4 * i] * inv, o[db][4 * i + 1] * inv, o[db][4 * i + 2] * inv, o[db][4 * i + 3] * inv};
+        *(f32x4*)(st + E::stage_write(db, i, lane_e)) = x;
+      }
+    __syncthreads();
+    float* const ob = p.out + sp.index * p.split_o + (int64_t)b * p.sob + (int64_t)h * p.soh;
+    const int q0 = qt * kFwdRows + wave * 32;
+#pragma unroll
+    for (int it0 = 0; it0 < E::kIters; it0 += 4) {
+      f32x4 x[4];  // four chunks read back before any is stored: one LDS latency
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x[j] = *(const f32x4*)(st + E::stage_read(it0 + j, lane_e));
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int qi = q0 + E::read_row(it0 + j, lane_e), ch = E::read_chunk(it0 + j, lane_e);
+        if (qi >= p.T || 4 * ch >= p.D) continue;
+        float* const o4 = ob + (int64_t)qi * p.sot + 4 * ch;
+        o4[0] = x[j].x;
+        o4[1] = x[j].y;
+        o4[2] = x[j].z;
+        o4[3] = x[j].w;
+      }
     }
-  if (g_e == 0) {
+  } else if (qi_e < p.T) {
+    float* orow = p.out + sp.index * p.split_o + (int64_t)b * p.sob + (int64_t)h * p.soh + (int64_t)qi_e * p.sot;
+#pragma unroll
+    for (int db = 0; db < DBLK; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int d = db * 32 + c_row(r, g_e);
+        if (d < p.D) orow[d] = o[db][r] * inv;
+      }
+  }
+  if (qi_e < p.T && g_e == 0) {
     const int64_t si = sp.index * p.split_ml + ((int64_t)b * p.H + h) * p.T + qi_e;
     const float m_nat = m_max * kLn2;
     if (p.m_bf16) {
@@ -735,20 +770,70 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
 
   const int lane_e = lane_id_fresh(), g_e = lane_e >> 5;  // as in the forward's epilogue
   const int qi_e = qt * kDqRows + wave * 32 + (lane_e & 31);
-  if (qi_e >= p.T) return;
-  char* drow = (char*)p.dq + ((sp.index * p.split_dq + (int64_t)b * p.sdqb + (int64_t)h * p.sdqh +
-                               (int64_t)qi_e * p.sdqt) << (p.dq_f32 ? 2 : 1));
+  using E = cq_epi::QRows<DP>;
+  if constexpr (E::kHalfBytes <= (int)sizeof(Ks) && E::kHalfBytes <= (int)sizeof(Vs)) {
+    // dQ staged through LDS as in the forward (cq_epilogue.h)
+    float* const st = (float*)(cq_epi::half(wave) ? &Vs[0][0][0] : &Ks[0][0][0]) + E::stage_base(wave);
+    __syncthreads();  // every wave is done with the loop's K / V tiles
 #pragma unroll
-  for (int db = 0; db < DBLK; ++db)
+    for (int db = 0; db < DBLK; ++db)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int d = db * 32 + c_row(r, g_e);
-      if (d < p.D) {
-        const float v = dq[db][r] * p.scale;
-        if (p.dq_f32) ((float*)drow)[d] = v;
-        else ((bf16*)drow)[d] = (bf16)v;
+      for (int i = 0; i < 4; ++i) {
+        const f32x4 x = {dq[db][4 * i] * p.scale, dq[db][4 * i + 1] * p.scale, dq[db][4 * i + 2] * p.scale,
+                         dq[db][4 * i + 3] * p.scale};
+        *(f32x4*)(st + E::stage_write(db, i, lane_e)) = x;
+      }
+    __syncthreads();
+    const int64_t bh = sp.index * p.split_dq + (int64_t)b * p.sdqb + (int64_t)h * p.sdqh;
+    const int q0 = qt * kDqRows + wave * 32;
+    // bf16 rows go out 8 bytes per lane when the view is 8-byte aligned,
+    // else one element per lane and store
+    const bool wide = p.dq_f32 || ((((uintptr_t)p.dq & 7u) == 0) && ((p.sdqb | p.sdqh | p.sdqt) & 3) == 0);
+    if (wide) {
+#pragma unroll
+      for (int it0 = 0; it0 < E::kIters; it0 += 4) {
+        f32x4 x[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x[j] = *(const f32x4*)(st + E::stage_read(it0 + j, lane_e));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int qi = q0 + E::read_row(it0 + j, lane_e), ch = E::read_chunk(it0 + j, lane_e);
+          if (qi >= p.T || 4 * ch >= p.D) continue;
+          const int64_t e = bh + (int64_t)qi * p.sdqt + 4 * ch;
+          if (p.dq_f32) {
+            float* const o4 = (float*)p.dq + e;
+            o4[0] = x[j].x;
+            o4[1] = x[j].y;
+            o4[2] = x[j].z;
+            o4[3] = x[j].w;
+          } else {
+            *(bf16x4*)((bf16*)p.dq + e) = __builtin_convertvector(x[j], bf16x4);
+          }
+        }
+      }
+    } else {
+#pragma unroll 4
+      for (int it = 0; it < E::kElemIters; ++it) {
+        const int qi = q0 + E::elem_row(it, lane_e), col = E::elem_col(it, lane_e);
+        const float x = st[E::stage_elem(it, lane_e)];
+        if (qi < p.T && col < p.D) ((bf16*)p.dq)[bh + (int64_t)qi * p.sdqt + col] = (bf16)x;
       }
     }
+  } else if (qi_e < p.T) {
+    char* drow = (char*)p.dq + ((sp.index * p.split_dq + (int64_t)b * p.sdqb + (int64_t)h * p.sdqh +
+                                 (int64_t)qi_e * p.sdqt) << (p.dq_f32 ? 2 : 1));
+#pragma unroll
+    for (int db = 0; db < DBLK; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int d = db * 32 + c_row(r, g_e);
+        if (d < p.D) {
+          const float v = dq[db][r] * p.scale;
+          if (p.dq_f32) ((float*)drow)[d] = v;
+          else ((bf16*)drow)[d] = (bf16)v;
+        }
+      }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -958,6 +1043,61 @@ __global__ __launch_bounds__(64 * kDkWaves, 1) void dkdv_kernel(BwdParams p) {
   // keys past the valid length (pads) get zero
   const int64_t base = (int64_t)b * p.sdkb + (int64_t)h * p.sdkh;
   const int lane_e = lane_id_fresh(), g_e = lane_e >> 5;  // as in the forward's epilogue
+  using E = cq_epi::KRows<DP>;
+  if constexpr (E::kHalfBytes <= (int)sizeof(QG) && E::kHalfBytes <= (int)sizeof(Vb)) {
+    // dK, then dV, staged through LDS (cq_epilogue.h: waves 0-3 in the Q / dO
+    // buffers, 4-7 in the V tiles) and stored as contiguous row pieces
+    float* const st = (float*)(cq_epi::half(wave) ? (void*)&Vb[0][0] : (void*)&QG[0][0][0]) + E::stage_base(wave);
+    const int rows_c = p.ct_rows[c];
+    // bf16 rows 8 bytes per lane when both views are 8-byte aligned, else one
+    // element per lane and store
+    const bool wide = p.dkv_f32 || (((((uintptr_t)p.ct.dk[c]) | ((uintptr_t)p.ct.dv[c])) & 7u) == 0 &&
+                                    ((p.sdkb | p.sdkh | p.sdkt) & 3) == 0);
+    __syncthreads();  // every wave is done with the loop's LDS
+#pragma unroll
+    for (int tn = 0; tn < 2; ++tn) {
+      const float sc = tn == 0 ? p.scale : 1.f;
+#pragma unroll
+      for (int db = 0; db < DBLK; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) st[E::stage_write(db, r, lane_e)] = (tn == 0 ? dk[db][r] : dv[db][r]) * sc;
+      __syncthreads();
+      void* const outp = tn == 0 ? (void*)p.ct.dk[c] : (void*)p.ct.dv[c];
+      if (wide) {
+#pragma unroll
+        for (int it0 = 0; it0 < E::kIters; it0 += 4) {
+          f32x4 x[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) x[j] = *(const f32x4*)(st + E::stage_read(it0 + j, lane_e));
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int kk = key0 + E::read_row(it0 + j, lane_e), ch = E::read_chunk(it0 + j, lane_e);
+            if (kk >= rows_c || 4 * ch >= p.D) continue;
+            const f32x4 y = kk < len ? x[j] : f32x4{0.f, 0.f, 0.f, 0.f};
+            const int64_t e = base + (int64_t)kk * p.sdkt + 4 * ch;
+            if (p.dkv_f32) {
+              float* const o4 = (float*)outp + e;
+              o4[0] = y.x;
+              o4[1] = y.y;
+              o4[2] = y.z;
+              o4[3] = y.w;
+            } else {
+              *(bf16x4*)((bf16*)outp + e) = __builtin_convertvector(y, bf16x4);
+            }
+          }
+        }
+      } else {
+#pragma unroll 4
+        for (int it = 0; it < E::kElemIters; ++it) {
+          const int kk = key0 + E::elem_row(it, lane_e), col = E::elem_col(it, lane_e);
+          const float x = st[E::stage_elem(it, lane_e)];
+          if (kk < rows_c && col < p.D) ((bf16*)outp)[base + (int64_t)kk * p.sdkt + col] = (bf16)(kk < len ? x : 0.f);
+        }
+      }
+      __syncthreads();  // the staging rows are rewritten with dV
+    }
+    return;
+  }
 #pragma unroll
   for (int db = 0; db < DBLK; ++db) {
     const int d = db * 32 + (lane_e & 31);
