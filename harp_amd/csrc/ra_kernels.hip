@@ -297,8 +297,8 @@ __device__ __forceinline__ float row_bcast(float x, int r) {  // r must fold to 
 constexpr int kFwdWaves = 8;
 constexpr int kFwdRows = 32 * kFwdWaves;
 static_assert(kFwdRows == kQueryBlockRows, "the host sizes KV splits with kQueryBlockRows");
-// Keys per tile = 64 * kFwdSub: fewer barriers, pipeline fills and row-max
-// passes per key; the block's LDS holds two such K / V tiles.
+// Keys per tile = 64 * kFwdSub: fewer barriers, pipeline fills and rescale
+// tests per key; the block's LDS holds two such K / V tiles.
 constexpr int kFwdSub = 2;
 // KSTEPS = ceil(D/16) k-steps of the S contraction; DBLK = ceil(D/32) row
 // blocks of O^T (DP = 32*DBLK >= 16*KSTEPS).  Block = kFwdWaves waves x 32 queries;
@@ -308,7 +308,7 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
   constexpr int DP = DBLK * 32;
   using GK = XorTile<DP>;  // K: row fragments only
   using GV = XorTile<DP>;  // V: transposed fragments
-  constexpr float kTau = 8.f;  // lazy-rescale threshold (log2 units): P <= 2^8
+  constexpr float kTauExp = 256.f;  // lazy-rescale threshold: a lane's tile sum of P above 2^8
   constexpr int NS = kFwdSub, KB = 2 * NS;  // 64-row sub-tiles, 32-key blocks per tile
   __shared__ __attribute__((aligned(16))) bf16 Ks[2][NS][GK::ELEMS];
   __shared__ __attribute__((aligned(16))) bf16 Vs[2][NS][GV::ELEMS];
@@ -344,9 +344,10 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
   f32x16 o[DBLK];
 #pragma unroll
   for (int i = 0; i < DBLK; ++i) o[i] = zero16();
-  float m_ref = -INFINITY;  // reference point of P (log2 domain), lags the max by < kTau
-  float m_max = -INFINITY;  // exact running max of s*c2
-  float l_run = 0.f;        // this lane-half's partial sum of exp2(s*c2 - m_ref)
+  // reference point of P (log2 domain): the first keys of a row overflow
+  // their exps against -FLT_MAX, which makes the tile rescale
+  float m_ref = -__FLT_MAX__;
+  float l_run = 0.f;  // this lane-half's partial sum of exp2(s*c2 - m_ref)
 
   const int64_t kvo = (int64_t)b * p.skb + (int64_t)h * p.skh;
   auto issue = [&](const KvCursor& t, int bf) {
@@ -421,37 +422,45 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
     }
 
     prio<2>();
-    // online softmax, lane = query
-    float mx = -INFINITY;
+    // online softmax, lane = query: the exps run against the current
+    // reference point at once, and the test looks at their sum.  A lane
+    // whose tile sum passes 2^8 (some exp above it, or overflowed) makes the
+    // wave move its reference points up to the tile's row maxima, rescale O
+    // and l, and compute the tile's exps again; otherwise every exp is at
+    // most 2^8.  No max / compare chain runs before the exps.
+    bf16x8 pf[2 * KB];
+    auto tile_exps = [&]() {
+      float bs = 0.f;
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb)
+      for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
-    mx = wave_half_max(mx) * c2;
-    m_max = fmaxf(m_max, mx);
-    if (__any(mx > m_ref + kTau)) {
-      const float m_new = fmaxf(m_ref, mx);
-      const float corr = fast_exp2(m_ref - (m_new == -INFINITY ? 0.f : m_new));
+        for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float e = fast_exp2(__builtin_fmaf(s[kb][hf * 8 + j], c2, -m_ref));
+            bs += e;
+            pf[kb * 2 + hf][j] = (bf16)e;
+          }
+      return bs;
+    };
+    float bs = tile_exps();
+    if (__any(bs > kTauExp)) {  // rare: the first tile of a row, or a jump of the row max
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
+      const float m_new = fmaxf(m_ref, wave_half_max(mx) * c2);
+      const float corr = fast_exp2(m_ref - m_new);
       l_run *= corr;
 #pragma unroll
       for (int i = 0; i < DBLK; ++i)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[i][r] *= corr;
       m_ref = m_new;
+      bs = tile_exps();
     }
-    const float m_use = (m_ref == -INFINITY) ? 0.f : m_ref;
-
-    bf16x8 pf[2 * KB];
-#pragma unroll
-    for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-      for (int hf = 0; hf < 2; ++hf)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float e = fast_exp2(__builtin_fmaf(s[kb][hf * 8 + j], c2, -m_use));
-          l_run += e;
-          pf[kb * 2 + hf][j] = (bf16)e;
-        }
+    l_run += bs;
 
     prio<1>();
     // O^T += V^T P^T; step i = (ks2 = i / DBLK, db = i % DBLK), 16 keys per ks2
@@ -464,11 +473,10 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
     cur = nxt;
   }
 
-  // l relative to the exact max: l * 2^(m_ref - m_max)
-  float l_tot = wave_half_sum(l_run);
-  const float shift = (m_max == -INFINITY) ? 1.f : fast_exp2(m_ref - m_max);
+  // m = the reference point (a row without keys: m = -inf, l = 0), l relative to it
+  const float l_tot = wave_half_sum(l_run);
   const float inv = (l_tot > 0.f) ? 1.f / l_tot : 0.f;
-  l_tot *= shift;
+  const float m_out = (l_tot > 0.f) ? m_ref : -INFINITY;
   // lane-dependent indices again, from a fresh lane id (nothing kept live
   // across the loop for them)
   const int lane_e = lane_id_fresh(), g_e = lane_e >> 5;
@@ -518,7 +526,7 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
   }
   if (qi_e < p.T && g_e == 0) {
     const int64_t si = sp.index * p.split_ml + ((int64_t)b * p.H + h) * p.T + qi_e;
-    const float m_nat = m_max * kLn2;
+    const float m_nat = m_out * kLn2;
     if (p.m_bf16) {
       const bf16 mh = (bf16)m_nat;
       const float mhf = (float)mh;
@@ -688,6 +696,14 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
   float lse2_s = lse2, dlt_s = dlt;
   settle(lse2_s);
   settle(dlt_s);
+  // -D, the dP^T accumulators' initial value (one value per lane: its
+  // query), so dP - D comes out of the MFMAs and dS costs one multiply;
+  // at four d blocks its 16 registers do not fit beside the rest, and dS
+  // subtracts D instead
+  constexpr bool kDInit = DBLK <= 3;
+  f32x16 neg_d;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) neg_d[r] = kDInit ? -dlt_s : 0.f;
 #pragma unroll 1
   while (cur.step < sp.end) {
     const KvCursor nxt = kv_next(p.ct, kvo, cur, 64 * NS, sp.end);
@@ -701,11 +717,12 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
     f32x16 s[2], dp[2];
     bf16x8 dsf[2][2];
     // B(j), rows r0 .. r0+NR-1: dS^T = P^T (dP^T - D), P^T = exp2(S^T c2 - LSE2)
+    // (the dP^T accumulators start at -D)
     auto softmax_rows = [&](int j, int r0, int nr) {
 #pragma unroll
       for (int r = r0; r < r0 + nr; ++r) {
         const float pv = exp2_unit(__builtin_fmaf(s[j & 1][r], c2, -lse2_s));
-        dsf[j & 1][r >> 3][r & 7] = (bf16)(pv * (dp[j & 1][r] - dlt_s));
+        dsf[j & 1][r >> 3][r & 7] = (bf16)(pv * (kDInit ? dp[j & 1][r] : dp[j & 1][r] - dlt_s));
       }
     };
     // A(j), with B(jb) spread over its KSTEPS steps (jb < 0: none)
@@ -714,7 +731,7 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
       const bf16* K = Ks[buf][j / 2];
       const bf16* V = Vs[buf][j / 2];
       s[j & 1] = zero16();
-      dp[j & 1] = zero16();
+      dp[j & 1] = kDInit ? neg_d : zero16();
       constexpr int kRowsPerStep = (16 + KSTEPS - 1) / KSTEPS;
       pipelined<KSTEPS, kDqPfA>(
           [&](int ks) { return Frag2{klo.row_frag_lean(K, j & 1, ks), vlo.row_frag_lean(V, j & 1, ks)}; },
