@@ -51,13 +51,12 @@ enum { HARP_RA_F32 = 0, HARP_RA_BF16 = 1 };
 
 /*
  * Forward: O = softmax(scale * Q K^T) V over all sp_size chunks, with
- * O written as fp32 (divided by l), m_i a reference point of the row
- * (natural-log domain; fp32, or bf16 when m_i_dtype == HARP_RA_BF16) and
- * l_i = sum exp(scale*Q K^T - m_i), so that m_i + log(l_i) = LSE exactly for
- * either m_i dtype.  m_i is the reference point of the kernel's exps, at
- * most 8 ln 2 below the row max of scale*Q K^T (the reference's m_i is that
- * max; only m_i + log(l_i) is consumed).  A row without keys gets
- * m_i = -inf, l_i = 0.
+ * O written as fp32 (divided by l), m_i (natural-log domain; fp32, or bf16
+ * when m_i_dtype == HARP_RA_BF16) and l_i = sum exp(scale*Q K^T - m_i), so
+ * that m_i + log(l_i) = LSE exactly for either m_i dtype.  m_i is the
+ * reference point of the kernel's exps, at most 8 ln 2 below the row max of
+ * scale*Q K^T (the reference's m_i is that max; only m_i + log(l_i) is
+ * consumed).  A row without keys gets m_i = -inf, l_i = 0.
  * Replaces: ring_attention_forward(__bf16* Q, __bf16* K, __bf16* V, float* out,
  *   int t_num, int h_num, int h_len, int sp_size, __bf16* m_i, float* l_i,
  *   float scale)  — gemm/ring_attention/ring_attn.cpp:2412-2414, called from
