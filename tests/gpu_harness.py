@@ -37,13 +37,15 @@ def run_hip(
     grad_dtype: torch.dtype = torch.bfloat16,
     backward: bool = True,
     dkv_view: Optional[tuple] = None,
+    dq_view: Optional[tuple] = None,
 ) -> Dict[str, torch.Tensor]:
     """Run forward (+ delta + backward) on the GPU; return CPU tensors:
     o (fp32), lse (fp64), m, l, delta, dq, dk, dv (dk/dv concatenated over chunks).
     dkv_view = (pad, offset) (C ABI only): each dK / dV chunk is the view
     [..., offset:offset + D] of a token-major buffer whose rows hold D + pad
     elements per head, so the view's row stride is H (D + pad) and its base
-    sits `offset` elements into the buffer."""
+    sits `offset` elements into the buffer.  dq_view = (pad, offset): the same
+    for dQ (C ABI only)."""
     dev = torch.device("cuda")
     B, H, T, D = q.shape
     n = len(ks)
@@ -75,7 +77,12 @@ def run_hip(
         if via == "abi":
             delta = torch.empty((B, H, T, 1), device=dev, dtype=torch.float32)
             hops.abi_delta(dod, out, delta)
-            dq = torch.full((B, T, H, D), float("nan"), device=dev, dtype=grad_dtype).transpose(1, 2)
+            if dq_view is not None:
+                pad, off = dq_view
+                dq = torch.full((B, T, H, D + pad), float("nan"), device=dev, dtype=grad_dtype)[..., off:off + D]
+                dq = dq.transpose(1, 2)
+            else:
+                dq = torch.full((B, T, H, D), float("nan"), device=dev, dtype=grad_dtype).transpose(1, 2)
 
             def grad_chunk():
                 if dkv_view is not None:
@@ -91,7 +98,7 @@ def run_hip(
             dk_all = torch.cat(dk, dim=2)
             dv_all = torch.cat(dv, dim=2)
         else:
-            assert dkv_view is None, "dkv_view goes through the C ABI"
+            assert dkv_view is None and dq_view is None, "dkv_view / dq_view go through the C ABI"
             delta = torch.ops.ring_attention_ops.ring_attention_delta(dod, out)
             dq = torch.full((B, T, H, D), float("nan"), device=dev, dtype=grad_dtype).transpose(1, 2)
             dk_all = torch.full((B, n * tc, H, D), float("nan"), device=dev, dtype=grad_dtype).transpose(1, 2)

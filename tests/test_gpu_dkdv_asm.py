@@ -119,6 +119,23 @@ def test_unaligned_dk_dv_views_head_dim_64(grad_dtype):
     _views_match(64, (1, 1), grad_dtype, seed=34)
 
 
+@pytest.mark.parametrize("heads", [3, 72])  # 6 query tiles: KV split and merge; 144: the kernel's own stores
+@pytest.mark.parametrize("head_dim,view", [(64, (1, 1)), (72, (3, 1)), (128, (4, 0))])
+@pytest.mark.parametrize("grad_dtype", [torch.bfloat16, torch.float32])
+def test_strided_dq_views(head_dim, view, grad_dtype, heads):
+    """dQ written into a strided view equals the plain call's bit for bit:
+    at head dims 64 and 72 (the compiled dQ kernel) at an odd element offset
+    with an odd row stride (bf16 rows only 2-byte aligned: stored one element
+    per lane), at 128 with padded, 8-byte aligned rows (the C ABI refuses
+    other bf16 dQ views there)."""
+    print(f"[dq strided views D={head_dim} {view} {grad_dtype} H={heads}]", flush=True)
+    q, ks, vs, do = orc.make_inputs(1, heads, 300, head_dim, 2, seed=35, chunk_len=200)
+    scale = 1.0 / math.sqrt(head_dim)
+    res = run_hip(q, ks, vs, do, scale, grad_dtype=grad_dtype)
+    got = run_hip(q, ks, vs, do, scale, grad_dtype=grad_dtype, dq_view=view)
+    assert torch.equal(res["dq"], got["dq"])
+
+
 @pytest.mark.skip(reason="head dim 128 stores bf16 dK / dV 8 bytes per lane: the C ABI refuses chunks that are not "
                          "8-byte aligned or strides that are not multiples of 4 elements (HARP_RA_EINVAL, "
                          "tests/test_abi.py); a version of the epilogue with element-store fallbacks for such rows "
