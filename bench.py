@@ -13,7 +13,10 @@ input and output resident in HBM.  FLOP_total = 14*B*H*T*L*D (fwd 4, bwd 10;
 L = valid keys).
 
 Prints ONE JSON line.  --gpus N with N > 1 is refused: this build measures one
-GPU (multi-GPU sharding is a design, not a measured path).
+GPU (multi-GPU sharding is a design, not a measured path).  After the headline
+(config 4) it adds, as context: BASELINE configs 2, 3 and 5 (`other_configs`)
+and HARP's own call shapes, 30 heads of 128 with 256 or 768 local rows over 8
+ring steps (`harp_call_shapes`).
 """
 
 from __future__ import annotations
@@ -32,7 +35,7 @@ PEAK_HBM_GBS = 8000.0
 # with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE, each scaled by what the same
 # counter reads for a 1 GiB device copy in the same run (FETCH x2.0, WRITE
 # x1.0).  Source: profiles/ring_attn_config4_counters.md.
-MEASURED_TRAFFIC_BYTES = {4: {"fwd": 961.0e6, "dkdv": 2429.1e6, "dq": 958.6e6, "delta": 151.8e6, "stats": 3.6e6}}
+MEASURED_TRAFFIC_BYTES = {4: {"fwd": 958.4e6, "dkdv": 2429.0e6, "dq": 961.2e6, "delta": 151.8e6, "stats": 3.6e6}}
 
 CONFIGS = {
     1: dict(B=1, H=8, T=512, D=64, N=1, tc=512, lens=None, vscale=1.0),
@@ -40,6 +43,12 @@ CONFIGS = {
     3: dict(B=2, H=16, T=4096, D=72, N=8, tc=4096, lens=None, vscale=0.5),
     4: dict(B=1, H=24, T=8192, D=128, N=8, tc=8192, lens=None, vscale=1.0),
     5: dict(B=1, H=24, T=4429, D=128, N=4, tc=4480, lens=[4429] * 4, vscale=1.0),
+}
+# HARP's own per-rank call shapes (30 heads of 128, 256 / 768 local rows, an
+# 8-rank ring): context beside the BASELINE configs, not a bench line
+HARP_SHAPES = {
+    "T256": dict(B=1, H=30, T=256, D=128, N=8, tc=256, lens=None, vscale=1.0),
+    "T768": dict(B=1, H=30, T=768, D=128, N=8, tc=768, lens=None, vscale=1.0),
 }
 
 
@@ -580,15 +589,15 @@ class Workload:
         return {"ms": ev[0].elapsed_time(ev[-1]) / steps, "median_ms": med, "kernels": kt, "wall_s": wall_s}
 
 
-def other_configs(ids, seed, dev, steps: int = 10, warmup: int = 3) -> dict:
+def other_configs(ids, seed, dev, steps: int = 10, warmup: int = 3, table=None) -> dict:
     """The other BASELINE configs that run on the GPU (parity cases, not the
-    headline): ms per fwd+bwd step, counted TFLOP/s and % of the bf16 peak,
-    and each kernel's ms per step."""
+    headline), or other named shapes (`table`): ms per fwd+bwd step, counted
+    TFLOP/s and % of the bf16 peak, and each kernel's ms per step."""
     import torch
 
     res = {}
     for cid in ids:
-        cfg = CONFIGS[cid]
+        cfg = (table or CONFIGS)[cid]
         w = Workload(cfg, seed, dev)
         r = w.timed(steps, warmup)
         tf = 14.0 * bhtld_of(cfg) / (r["ms"] * 1e-3) / 1e12
@@ -621,6 +630,8 @@ def main() -> int:
     ap.add_argument("--no-telemetry", action="store_true", help="skip the board power / clock readings")
     ap.add_argument("--no-other-configs", action="store_true",
                     help="skip BASELINE configs 2, 3 and 5 after the headline (config 4) run")
+    ap.add_argument("--no-harp-shapes", action="store_true",
+                    help="skip HARP's own call shapes (H 30, D 128, T 256 / 768, 8 ring steps) after the headline")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="before the timed steps, run one plain device copy of this many MiB "
                          "(a known-size reference for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -755,6 +766,10 @@ def main() -> int:
         torch.cuda.empty_cache()
         result["other_configs"] = other_configs((2, 3, 5), args.seed, dev)
         print("bench: other configs done", file=sys.stderr, flush=True)
+    if args.config == 4 and not args.no_harp_shapes:
+        result["harp_call_shapes"] = other_configs(tuple(HARP_SHAPES), args.seed, dev, steps=20, warmup=5,
+                                                   table=HARP_SHAPES)
+        print("bench: HARP call shapes done", file=sys.stderr, flush=True)
     if not args.no_producer:
         prod = producer_bench(cfg, args.seed)
         rows = B * H * T
