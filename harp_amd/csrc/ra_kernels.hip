@@ -1138,36 +1138,36 @@ __global__ __launch_bounds__(64 * kDkWaves, 1) void dkdv_kernel(BwdParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// KV-split merges: 16 lanes per query row, 8 elements of D per lane.  The
-// splits are read kMergeGroup at a time, all loads of a group issued before
-// any is used (an index past the last split reads the last one again and is
-// given no weight), so a merge of n splits waits for ceil(n / 8) load
-// latencies instead of n.
+// KV-split merges: LPR lanes per query row (16, or 8 when D <= 64), 8
+// elements of D per lane.  The splits are read G at a time (G = the split
+// count up to 8), all loads of a group issued before any is used (an index
+// past the last split reads the last one again and is given no weight), so a
+// merge of n splits waits for ceil(n / 8) load latencies instead of n.
 // ---------------------------------------------------------------------------
-constexpr int kMergeGroup = 8;
-
+template <int G, int LPR>
 __global__ __launch_bounds__(256) void fwd_merge_kernel(FwdMergeParams p) {
+  constexpr int kRowsPerBlock = 256 / LPR;
   const int64_t rows = (int64_t)p.B * p.H * p.T;
-  const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
-  const int sub = threadIdx.x & 15, d0 = sub * 8;
-  if (row >= rows) return;  // whole 16-lane groups
+  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x / LPR);
+  const int sub = threadIdx.x % LPR, d0 = sub * 8;
+  if (row >= rows) return;  // whole LPR-lane groups
   const bool has_d = d0 < p.D;
   const int dr = has_d ? d0 : 0;  // lanes past D read (and drop) elements 0..7
   float mx = -INFINITY;
-  for (int s0 = 0; s0 < p.n_split; s0 += kMergeGroup) {
-    float ms[kMergeGroup];
+  for (int s0 = 0; s0 < p.n_split; s0 += G) {
+    float ms[G];
 #pragma unroll
-    for (int u = 0; u < kMergeGroup; ++u) ms[u] = p.part_m[min(s0 + u, p.n_split - 1) * rows + row];
+    for (int u = 0; u < G; ++u) ms[u] = p.part_m[min(s0 + u, p.n_split - 1) * rows + row];
 #pragma unroll
-    for (int u = 0; u < kMergeGroup; ++u) mx = fmaxf(mx, ms[u]);  // a repeated split changes no maximum
+    for (int u = 0; u < G; ++u) mx = fmaxf(mx, ms[u]);  // a repeated split changes no maximum
   }
   float l = 0.f, acc[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) acc[j] = 0.f;
-  for (int s0 = 0; s0 < p.n_split; s0 += kMergeGroup) {
-    float ms[kMergeGroup], ls[kMergeGroup], o[kMergeGroup][8];
+  for (int s0 = 0; s0 < p.n_split; s0 += G) {
+    float ms[G], ls[G], o[G][8];
 #pragma unroll
-    for (int u = 0; u < kMergeGroup; ++u) {
+    for (int u = 0; u < G; ++u) {
       const int64_t sr = min(s0 + u, p.n_split - 1) * rows + row;
       ms[u] = p.part_m[sr];
       ls[u] = p.part_l[sr];
@@ -1176,7 +1176,7 @@ __global__ __launch_bounds__(256) void fwd_merge_kernel(FwdMergeParams p) {
       for (int j = 0; j < 8; ++j) o[u][j] = op[j];
     }
 #pragma unroll
-    for (int u = 0; u < kMergeGroup; ++u) {
+    for (int u = 0; u < G; ++u) {
       if (s0 + u >= p.n_split) break;
       // a split without keys (l = 0) adds nothing; NaN statistics propagate
       const float w = (ls[u] == 0.f) ? 0.f : ls[u] * __expf(ms[u] - mx);
@@ -1209,24 +1209,26 @@ __global__ __launch_bounds__(256) void fwd_merge_kernel(FwdMergeParams p) {
   }
 }
 
+template <int G, int LPR>
 __global__ __launch_bounds__(256) void dq_merge_kernel(DqMergeParams p) {
+  constexpr int kRowsPerBlock = 256 / LPR;
   const int64_t rows = (int64_t)p.B * p.H * p.T;
-  const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
-  const int d0 = (threadIdx.x & 15) * 8;
+  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x / LPR);
+  const int d0 = (threadIdx.x % LPR) * 8;
   if (row >= rows || d0 >= p.D) return;
   float acc[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) acc[j] = 0.f;
-  for (int s0 = 0; s0 < p.n_split; s0 += kMergeGroup) {
-    float o[kMergeGroup][8];
+  for (int s0 = 0; s0 < p.n_split; s0 += G) {
+    float o[G][8];
 #pragma unroll
-    for (int u = 0; u < kMergeGroup; ++u) {
+    for (int u = 0; u < G; ++u) {
       const float* op = p.part + (min(s0 + u, p.n_split - 1) * rows + row) * p.D + d0;
 #pragma unroll
       for (int j = 0; j < 8; ++j) o[u][j] = op[j];
     }
 #pragma unroll
-    for (int u = 0; u < kMergeGroup; ++u) {
+    for (int u = 0; u < G; ++u) {
       if (s0 + u >= p.n_split) break;
 #pragma unroll
       for (int j = 0; j < 8; ++j) acc[j] += o[u][j];
@@ -1243,16 +1245,47 @@ __global__ __launch_bounds__(256) void dq_merge_kernel(DqMergeParams p) {
   }
 }
 
-hipError_t launch_fwd_merge(const FwdMergeParams& p, hipStream_t st) {
+namespace {
+
+// The merge instance for this split count and head dim: group = splits (2..8;
+// more splits go 8 at a time), 8 lanes per row when D <= 64 (16 otherwise).
+template <template <int, int> class K, class P>
+hipError_t launch_merge(const P& p, hipStream_t st) {
   const int64_t rows = (int64_t)p.B * p.H * p.T;
-  hipLaunchKernelGGL(fwd_merge_kernel, dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, st, p);
+  const bool narrow = p.D <= 64;
+  const int rpb = narrow ? 32 : 16;
+  const dim3 grid((unsigned)((rows + rpb - 1) / rpb)), block(256);
+  const int g = p.n_split < 2 ? 2 : (p.n_split > 8 ? 8 : p.n_split);
+#define HARP_MERGE_CASE(G)                                                         \
+  case G:                                                                          \
+    if (narrow) hipLaunchKernelGGL((K<G, 8>::kernel), grid, block, 0, st, p);     \
+    else hipLaunchKernelGGL((K<G, 16>::kernel), grid, block, 0, st, p);           \
+    break;
+  switch (g) {
+    HARP_MERGE_CASE(2)
+    HARP_MERGE_CASE(3)
+    HARP_MERGE_CASE(4)
+    HARP_MERGE_CASE(5)
+    HARP_MERGE_CASE(6)
+    HARP_MERGE_CASE(7)
+    default: HARP_MERGE_CASE(8)
+  }
+#undef HARP_MERGE_CASE
   return hipGetLastError();
 }
-hipError_t launch_dq_merge(const DqMergeParams& p, hipStream_t st) {
-  const int64_t rows = (int64_t)p.B * p.H * p.T;
-  hipLaunchKernelGGL(dq_merge_kernel, dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, st, p);
-  return hipGetLastError();
-}
+template <int G, int LPR>
+struct FwdMergeK {
+  static constexpr auto kernel = fwd_merge_kernel<G, LPR>;
+};
+template <int G, int LPR>
+struct DqMergeK {
+  static constexpr auto kernel = dq_merge_kernel<G, LPR>;
+};
+
+}  // namespace
+
+hipError_t launch_fwd_merge(const FwdMergeParams& p, hipStream_t st) { return launch_merge<FwdMergeK>(p, st); }
+hipError_t launch_dq_merge(const DqMergeParams& p, hipStream_t st) { return launch_merge<DqMergeK>(p, st); }
 
 hipError_t launch_stats_prep(const BwdParams& p, hipStream_t st) {
   const int64_t n = (int64_t)p.B * p.H * p.T;
