@@ -553,29 +553,38 @@ class Workload:
         self.backward()
 
     def timed(self, steps: int, warmup: int) -> dict:
-        """warmup untimed steps, then `steps` timed ones (HIP events on the
-        current stream, one per step, nothing else recorded in between: the
-        step time is the operators' own), then `steps` more with the
-        library's per-kernel launch timing on (its event pairs around every
-        launch add gaps to the stream, so those steps only give the per-kernel
-        breakdown).  Returns ms per step (mean and median of the first timed
-        steps), per-kernel (ms, launches) of the second, and the host wall
-        time of the first."""
+        """warmup untimed steps, then `steps` timed ones between one pair of
+        HIP events on the current stream (nothing else recorded in between:
+        the step time is the operators' own), then `steps` more with an event
+        after each (their median; an event between steps costs a few µs at
+        the smallest shapes, so those steps do not give the mean), then
+        `steps` more with the library's per-kernel launch timing on (its event
+        pairs around every launch add gaps to the stream, so those steps only
+        give the per-kernel breakdown).  Returns ms per step (mean over the
+        first timed steps, median of the second), per-kernel (ms, launches) of
+        the third, and the host wall time of the first."""
         import torch
 
         from harp_amd import _lib
 
         for _ in range(warmup):
             self.step()
-        ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         t_wall = time.perf_counter()
+        e0.record()
+        for _ in range(steps):
+            self.step()
+        e1.record()
+        torch.cuda.synchronize()
+        wall_s = time.perf_counter() - t_wall
+        ms = e0.elapsed_time(e1) / steps
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
         ev[0].record()
         for i in range(steps):
             self.step()
             ev[i + 1].record()
         torch.cuda.synchronize()
-        wall_s = time.perf_counter() - t_wall
         step_ms = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(steps))
         med = step_ms[len(step_ms) // 2] if len(step_ms) % 2 else 0.5 * (
             step_ms[len(step_ms) // 2 - 1] + step_ms[len(step_ms) // 2])
@@ -586,19 +595,30 @@ class Workload:
         torch.cuda.synchronize()
         _lib.timing_enable(False)
         kt = _lib.timing_read()
-        return {"ms": ev[0].elapsed_time(ev[-1]) / steps, "median_ms": med, "kernels": kt, "wall_s": wall_s}
+        return {"ms": ms, "median_ms": med, "kernels": kt, "wall_s": wall_s}
 
 
-def other_configs(ids, seed, dev, steps: int = 10, warmup: int = 3, table=None) -> dict:
+def other_configs(ids, seed, dev, min_steps: int = 10, table=None) -> dict:
     """The other BASELINE configs that run on the GPU (parity cases, not the
     headline), or other named shapes (`table`): ms per fwd+bwd step, counted
-    TFLOP/s and % of the bf16 peak, and each kernel's ms per step."""
+    TFLOP/s and % of the bf16 peak, and each kernel's ms per step.  Each
+    shape warms up for about 30 ms of its own steps (a few steps of a small
+    shape end before the board's clocks settle under the load) and times at
+    least `min_steps` steps and about 20 ms."""
     import torch
 
     res = {}
     for cid in ids:
         cfg = (table or CONFIGS)[cid]
         w = Workload(cfg, seed, dev)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(3):
+            w.step()
+        torch.cuda.synchronize()
+        est = max((time.perf_counter() - t0) / 3, 1e-5)
+        warmup = max(3, int(0.03 / est))
+        steps = max(min_steps, int(0.02 / est))
         r = w.timed(steps, warmup)
         tf = 14.0 * bhtld_of(cfg) / (r["ms"] * 1e-3) / 1e12
         res[str(cid)] = {
@@ -767,8 +787,7 @@ def main() -> int:
         result["other_configs"] = other_configs((2, 3, 5), args.seed, dev)
         print("bench: other configs done", file=sys.stderr, flush=True)
     if args.config == 4 and not args.no_harp_shapes:
-        result["harp_call_shapes"] = other_configs(tuple(HARP_SHAPES), args.seed, dev, steps=20, warmup=5,
-                                                   table=HARP_SHAPES)
+        result["harp_call_shapes"] = other_configs(tuple(HARP_SHAPES), args.seed, dev, table=HARP_SHAPES)
         print("bench: HARP call shapes done", file=sys.stderr, flush=True)
     if not args.no_producer:
         prod = producer_bench(cfg, args.seed)
