@@ -580,14 +580,8 @@ int harp_ra_backward(const void* q, const int64_t* q_strides, void* grad_q, cons
   char* ws = static_cast<char*>(workspace);
   p.stats = reinterpret_cast<float*>(ws + wl.stats);
   p.n_split = 1;
-  {
-    TimedLaunch tl(HARP_RA_KERNEL_STATS, st);
-    if ((rc = launched(launch_stats_prep(p, st), "statistics preparation"))) return rc;
-  }
-  {
-    TimedLaunch tl(HARP_RA_KERNEL_DKDV, st);
-    if ((rc = launched(launch_dkdv(p, st), "dK/dV"))) return rc;
-  }
+  // dQ first: it writes the per-query statistics planes the dK/dV kernel reads
+  BwdParams pk = p;
   DqMergeParams mp;
   std::memset(&mp, 0, sizeof(mp));
   if (wl.n_split > 1) {
@@ -615,6 +609,10 @@ int harp_ra_backward(const void* q, const int64_t* q_strides, void* grad_q, cons
     TimedLaunch tl(HARP_RA_KERNEL_DQ, st);  // the merge is timed with the dQ kernel
     if ((rc = launched(launch_dq(p, st), "dQ"))) return rc;
     if (wl.n_split > 1 && (rc = launched(launch_dq_merge(mp, st), "dQ merge"))) return rc;
+  }
+  {
+    TimedLaunch tl(HARP_RA_KERNEL_DKDV, st);
+    if ((rc = launched(launch_dkdv(pk, st), "dK/dV"))) return rc;
   }
   return ok();
 }

@@ -75,7 +75,7 @@ struct BwdParams {
   int m_bf16;
   const float* l;
   const float* delta;
-  float* stats;             // workspace [2][B*H*T]: -(m + ln l) / scale, -D (stats_prep_kernel)
+  float* stats;             // workspace [2][B*H*T]: -(m + ln l) / scale, -D (written by the dQ kernel)
   int n_split;              // KV splits of the dQ kernel (grid dimension y); > 1: dq is per-split partials
   int64_t split_dq;         // elements between the splits' dQ buffers
   int n_key_tiles;          // kDkdvBlockKeys-key blocks per (b, h) over all chunks
@@ -85,6 +85,16 @@ struct BwdParams {
   float inv_scale;  // 1 / scale (a kernel argument, so it stays in an SGPR)
   ChunkTable ct;
 };
+
+// The backward's per-query statistics.  The dQ kernel (split 0 of every
+// query tile) computes them for its rows, uses them and writes them to the
+// two planes of p.stats, which the dK/dV kernel, launched after it, reads:
+// plane 0 = -(m + ln l) / scale (-inf for a row without keys), plane 1 = -D.
+__device__ __forceinline__ float bwd_stat_lse(const BwdParams& p, int64_t i) {
+  const float mm = p.m_bf16 ? (float)((const bf16*)p.m)[i] : ((const float*)p.m)[i];
+  const float ll = p.l[i];
+  return (ll > 0.f) ? -(mm + __logf(ll)) * p.inv_scale : -INFINITY;
+}
 
 // Keys per dK/dV block (the host sizes the grid and the chunk table with it).
 constexpr int kDkdvBlockKeys = 256;
@@ -99,7 +109,6 @@ hipError_t launch_dq_merge(const DqMergeParams& p, hipStream_t st);
 // Query rows per block of the forward and dQ kernels (the host sizes KV splits with it).
 constexpr int kQueryBlockRows = 256;
 hipError_t launch_delta(const DeltaParams& p, hipStream_t st);
-hipError_t launch_stats_prep(const BwdParams& p, hipStream_t st);
 hipError_t launch_dq(const BwdParams& p, hipStream_t st);
 // the dQ kernel with the hand-scheduled main loop (dq_asm.hip), used by
 // launch_dq where it applies

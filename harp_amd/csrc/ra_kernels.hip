@@ -566,20 +566,13 @@ __global__ __launch_bounds__(256) void delta_kernel(DeltaParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Backward statistics, once per call, in the form both backward kernels read:
-// plane 0 = -(m + ln l) / scale per query (-inf for a row with l <= 0, which
-// then gets P = 0), plane 1 = -D.  With S' = Q K^T + plane 0 and
-// dP' = dO V^T + plane 1, P = exp2(S' c) and dS = P dP'.
+// Backward statistics, in the form both backward kernels use: plane 0 =
+// -(m + ln l) / scale per query (-inf for a row with l <= 0, which then gets
+// P = 0), plane 1 = -D.  With S' = Q K^T + plane 0 and dP' = dO V^T + plane 1,
+// P = exp2(S' c) and dS = P dP'.  The dQ kernel, launched first, computes
+// them for its rows (bwd_stat_lse) and writes the planes the dK/dV kernel
+// reads, so the backward needs no launch of its own for them.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void stats_prep_kernel(BwdParams p) {
-  const int64_t n = (int64_t)p.B * p.H * p.T;
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= n) return;
-  const float mm = p.m_bf16 ? (float)((const bf16*)p.m)[i] : ((const float*)p.m)[i];
-  const float ll = p.l[i];
-  p.stats[i] = (ll > 0.f) ? -(mm + __logf(ll)) * p.inv_scale : -INFINITY;
-  p.stats[n + i] = -p.delta[i];
-}
 
 // ---------------------------------------------------------------------------
 // Backward dQ (Q-stationary): dQ = scale * sum_c dS_c K_c
@@ -635,9 +628,16 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
   }
   const int64_t si = ((int64_t)b * p.H + h) * p.T + qi;
   const int64_t nrows = (int64_t)p.B * p.H * p.T;
+  // the row's statistics (bwd_stat_lse), written once for the dK/dV kernel;
   // LSE2 = -c * plane 0 (+inf for a row without keys); D = -plane 1
-  const float lse2 = q_ok ? -p.stats[si] * c2 : INFINITY;
-  const float dlt = q_ok ? -p.stats[nrows + si] : 0.f;
+  const float st0 = q_ok ? bwd_stat_lse(p, si) : 0.f;
+  const float st1 = q_ok ? -p.delta[si] : 0.f;
+  if (q_ok && g == 0 && sp.index == 0) {
+    p.stats[si] = st0;
+    p.stats[nrows + si] = st1;
+  }
+  const float lse2 = q_ok ? -st0 * c2 : INFINITY;
+  const float dlt = q_ok ? -st1 : 0.f;
   XorLanes<DP, KSTEPS> klo;
   klo.init_rows_lean(lane);
   klo.init_tr_lean(lane);
@@ -1286,12 +1286,6 @@ struct DqMergeK {
 
 hipError_t launch_fwd_merge(const FwdMergeParams& p, hipStream_t st) { return launch_merge<FwdMergeK>(p, st); }
 hipError_t launch_dq_merge(const DqMergeParams& p, hipStream_t st) { return launch_merge<DqMergeK>(p, st); }
-
-hipError_t launch_stats_prep(const BwdParams& p, hipStream_t st) {
-  const int64_t n = (int64_t)p.B * p.H * p.T;
-  hipLaunchKernelGGL(stats_prep_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, p);
-  return hipGetLastError();
-}
 
 // Every (KSTEPS, DBLK) variant the launchers dispatch to, instantiated
 // explicitly: with lambdas in the kernel bodies the host pass otherwise

@@ -154,7 +154,8 @@ HARP_RA_API const char* harp_ra_last_error(void);
  * last read, then clears them.  Not thread-safe with concurrent calls.
  */
 enum {
-  HARP_RA_KERNEL_STATS = 0, /* the backward's per-query statistics preparation */
+  HARP_RA_KERNEL_STATS = 0, /* kept for the numbering: the dQ kernel prepares the
+                               backward's statistics, so this kind counts no launches */
   HARP_RA_KERNEL_FWD = 1,
   HARP_RA_KERNEL_DELTA = 2,
   HARP_RA_KERNEL_DKDV = 3,

@@ -661,7 +661,8 @@ def _put_rows(regfile, base, rows_bf16, T, w):
 
 def run_dq_block(q, do, ks, vs, lens, order, stats0, stats1, scale, lines=None):
     """dQ of query rows 0..255 (T = len(q) <= 256) over the chunks; stats
-    planes as stats_prep_kernel writes them.  Returns dQ [T, 128] (scaled)."""
+    planes as the dQ kernel computes them (bwd_stat_lse and -D).  Returns dQ
+    [T, 128] (scaled)."""
     T = q.shape[0]
     mem = Mem()
     ops0 = _chunk_setup(mem, ks, vs, lens, order)
