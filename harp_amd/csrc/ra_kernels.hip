@@ -1153,19 +1153,9 @@ __global__ __launch_bounds__(256) void fwd_merge_kernel(FwdMergeParams p) {
   if (row >= rows) return;  // whole LPR-lane groups
   const bool has_d = d0 < p.D;
   const int dr = has_d ? d0 : 0;  // lanes past D read (and drop) elements 0..7
-  float mx = -INFINITY;
-  for (int s0 = 0; s0 < p.n_split; s0 += G) {
-    float ms[G];
-#pragma unroll
-    for (int u = 0; u < G; ++u) ms[u] = p.part_m[min(s0 + u, p.n_split - 1) * rows + row];
-#pragma unroll
-    for (int u = 0; u < G; ++u) mx = fmaxf(mx, ms[u]);  // a repeated split changes no maximum
-  }
-  float l = 0.f, acc[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) acc[j] = 0.f;
-  for (int s0 = 0; s0 < p.n_split; s0 += G) {
-    float ms[G], ls[G], o[G][8];
+  float ms[G], ls[G], o[G][8];
+  // splits s0 .. s0 + G - 1 (an index past the last split reads the last one again)
+  auto load_group = [&](int s0) {
 #pragma unroll
     for (int u = 0; u < G; ++u) {
       const int64_t sr = min(s0 + u, p.n_split - 1) * rows + row;
@@ -1175,9 +1165,14 @@ __global__ __launch_bounds__(256) void fwd_merge_kernel(FwdMergeParams p) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) o[u][j] = op[j];
     }
+  };
+  float mx = -INFINITY, l = 0.f, acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+  auto add_group = [&](int s0) {
 #pragma unroll
     for (int u = 0; u < G; ++u) {
-      if (s0 + u >= p.n_split) break;
+      if (s0 + u >= p.n_split) break;  // a repeated split gets no weight
       // a split without keys (l = 0) adds nothing; NaN statistics propagate
       const float w = (ls[u] == 0.f) ? 0.f : ls[u] * __expf(ms[u] - mx);
       l += w;
@@ -1185,6 +1180,21 @@ __global__ __launch_bounds__(256) void fwd_merge_kernel(FwdMergeParams p) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[j] += w * o[u][j];
       }
+    }
+  };
+  if (p.n_split <= G) {  // up to 8 splits: one round of loads, the maximum over the loaded m
+    load_group(0);
+#pragma unroll
+    for (int u = 0; u < G; ++u) mx = fmaxf(mx, ms[u]);  // a repeated split changes no maximum
+    add_group(0);
+  } else {  // more: the maximum first, then the groups again
+    for (int s0 = 0; s0 < p.n_split; s0 += G) {
+#pragma unroll
+      for (int u = 0; u < G; ++u) mx = fmaxf(mx, p.part_m[min(s0 + u, p.n_split - 1) * rows + row]);
+    }
+    for (int s0 = 0; s0 < p.n_split; s0 += G) {
+      load_group(s0);
+      add_group(s0);
     }
   }
   const int t = (int)(row % p.T);
