@@ -35,7 +35,7 @@ PEAK_HBM_GBS = 8000.0
 # with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE, each scaled by what the same
 # counter reads for a 1 GiB device copy in the same run (FETCH x2.0, WRITE
 # x1.0).  Source: profiles/ring_attn_config4_counters.md.
-MEASURED_TRAFFIC_BYTES = {4: {"fwd": 958.4e6, "dkdv": 2429.0e6, "dq": 961.2e6, "delta": 151.8e6, "stats": 3.6e6}}
+MEASURED_TRAFFIC_BYTES = {4: {"fwd": 960.3e6, "dkdv": 2429.0e6, "dq": 961.8e6, "delta": 151.8e6}}
 
 CONFIGS = {
     1: dict(B=1, H=8, T=512, D=64, N=1, tc=512, lens=None, vscale=1.0),
