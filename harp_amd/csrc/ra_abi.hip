@@ -185,9 +185,9 @@ size_t fwd_ws(int batch, int h_num, int t_num, int h_len, const Geometry& g) {
   return fwd_layout(batch, h_num, t_num, h_len, g).bytes;
 }
 
-// Backward: the per-query statistics, prepared once per call, in two fp32
-// planes of B*H*T rows; then, with KV splits, the dQ kernel's partials
-// (fp32 [n][B,H,T,D]).
+// Backward: the per-query statistics, written once per call by the dQ
+// kernel for the dK/dV kernel, in two fp32 planes of B*H*T rows; then, with
+// KV splits, the dQ kernel's partials (fp32 [n][B,H,T,D]).
 struct BwdLayout {
   int n_split;
   size_t stats, dq, bytes;  // byte offsets

@@ -270,6 +270,21 @@ def test_odd_sizes_and_empty_chunk():
 
 
 @pytest.mark.parametrize("D", [64, 128])  # compiled kernels; the hand-scheduled D = 128 loops
+def test_sixteen_chunks_split_sixteen_ways(D):
+    """The most chunks the ABI takes (16) on a grid of one query tile: the
+    forward and dQ split the ring steps 16 ways, so both merges take their
+    path for more than eight splits (the maximum over every split's m first,
+    then two groups of eight).  Ragged and empty chunks, ring rank 5."""
+    lens = [40, 0, 33, 40, 1, 40, 0, 17, 40, 40, 29, 0, 40, 8, 40, 40]
+    print(f"[16 chunks D={D}]", flush=True)
+    q, ks, vs, do = orc.make_inputs(1, 1, 100, D, len(lens), seed=16, chunk_len=40)
+    scale = 1.0 / math.sqrt(D)
+    res = run_hip(q, ks, vs, do, scale, ring_rank=5, kv_lens=lens)
+    ref = _oracle_full(q, ks, vs, do, scale, rank=5, lens=lens)
+    _check_all(res, ref)
+
+
+@pytest.mark.parametrize("D", [64, 128])  # compiled kernels; the hand-scheduled D = 128 loops
 @pytest.mark.parametrize("via", ["abi", "ops"])
 def test_very_negative_lse_with_pad_keys(via, D):
     """Rows whose every score is far below -88 (LSE about -120), with ragged
