@@ -11,8 +11,9 @@
 // rows of kSR floats.  Every row is then read back 16 bytes per lane, lanes
 // covering consecutive 4-element chunks of consecutive rows, and stored as
 // contiguous pieces of the output row instead of one element per lane and
-// instruction.  DP = 32 * (d blocks) is the padded head dim, D <= DP the real
-// one (a multiple of 8, so a 4-element chunk is all in or all out).
+// instruction.  DP = 32 * (d blocks), or 32 n + 16 with a 16-wide last
+// block, is the padded head dim, D <= DP the real one (a multiple of 8, so a
+// 4-element chunk is all in or all out).
 #pragma once
 
 #include <stdint.h>
@@ -34,7 +35,7 @@ struct Rows {
   static constexpr int kChunks = DP / 4;               // 16-byte chunks per row
   static constexpr int kIters = kRows * kChunks / 64;  // read-back iterations per lane
   static constexpr int kHalfBytes = 4 * kRows * kSR * 4;  // four waves' staging
-  static_assert(DP % 32 == 0 && (kRows * kChunks) % 64 == 0, "whole read-back iterations");
+  static_assert(DP % 16 == 0 && (kRows * kChunks) % 64 == 0, "whole read-back iterations");
   HARP_HD static int stage_base(int wave) { return (wave & 3) * kRows * kSR; }
   // read-back iteration it of lane `lane`: row and chunk within the wave's rows
   HARP_HD static int read_row(int it, int lane) { return (it * 64 + lane) / kChunks; }
@@ -67,6 +68,12 @@ template <int DP>
 struct KRows : Rows<DP, DP + 8> {
   HARP_HD static int stage_write(int db, int r, int lane) {
     return c_row(r, lane >> 5) * (DP + 8) + db * 32 + (lane & 31);
+  }
+  // a 16-wide last d block (DP = 32 n + 16), 16 x 16 accumulator layout:
+  // register i of lane `lane` in tile t is key row 16 t + 4 (lane / 16) + i,
+  // column DP - 16 + lane % 16
+  HARP_HD static int stage_write_tail(int t, int i, int lane) {
+    return (16 * t + 4 * (lane >> 4) + i) * (DP + 8) + DP - 16 + (lane & 15);
   }
 };
 

@@ -42,6 +42,27 @@ struct ChunkTable {
 __device__ __forceinline__ f32x16 mfma32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
+// 16 x 16 x 32: lane L holds A row L % 16, B column L % 16, each with
+// k = 8 (L / 16) .. + 7; C column L % 16, rows 4 (L / 16) .. + 3 (measured on
+// the MI355X with an in-bounds probe, as v_permlane16_swap's lane exchange)
+__device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+// v_permlane16_swap on each dword of two fragments: afterwards x holds
+// (x row 0, y row 0, x row 2, y row 2) and y (x row 1, y row 1, x row 3,
+// y row 3), rows being the wave's four 16-lane groups
+__device__ __forceinline__ void permlane16_swap(bf16x8& x, bf16x8& y) {
+  typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+  u32x4 a = __builtin_bit_cast(u32x4, x), b = __builtin_bit_cast(u32x4, y);
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const auto r = __builtin_amdgcn_permlane16_swap(a[w], b[w], false, false);
+    a[w] = r[0];
+    b[w] = r[1];
+  }
+  x = __builtin_bit_cast(bf16x8, a);
+  y = __builtin_bit_cast(bf16x8, b);
+}
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 

@@ -498,6 +498,7 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
     __syncthreads();
     float* const ob = p.out + sp.index * p.split_o + (int64_t)b * p.sob + (int64_t)h * p.soh;
     const int q0 = qt * kFwdRows + wave * 32;
+    static_assert(E::kIters % 4 == 0, "read back in whole groups of four");
 #pragma unroll
     for (int it0 = 0; it0 < E::kIters; it0 += 4) {
       f32x4 x[4];  // four chunks read back before any is stored: one LDS latency
@@ -807,6 +808,7 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
     // else one element per lane and store
     const bool wide = p.dq_f32 || ((((uintptr_t)p.dq & 7u) == 0) && ((p.sdqb | p.sdqh | p.sdqt) & 3) == 0);
     if (wide) {
+      static_assert(E::kIters % 4 == 0, "read back in whole groups of four");
 #pragma unroll
       for (int it0 = 0; it0 < E::kIters; it0 += 4) {
         f32x4 x[4];
@@ -878,8 +880,13 @@ constexpr int kDkWaves = kDkdvBlockKeys / 32;
 template <int KSTEPS, int DBLK>
 __global__ __launch_bounds__(64 * kDkWaves, 1) void dkdv_kernel(BwdParams p) {
   constexpr int DP = DBLK * 32;
-  using GV = PadTile<DP>;  // the block's V rows: row fragments only
-  using GQ = XorTile<DP>;  // Q / dO tiles: row and transposed fragments
+  // At 5 k-steps (head dims 72 and 80) the last d block of dK / dV is 16 wide:
+  // 16 x 16 x 32 MFMAs over d 64-79 instead of 32 x 32 x 16 ones over 64-95.
+  constexpr bool kTail = KSTEPS == 5 && DBLK == 3;
+  constexpr int DBF = kTail ? DBLK - 1 : DBLK;  // 32-wide d blocks
+  constexpr int DPE = kTail ? 80 : DP;          // d columns the tiles and outputs hold
+  using GV = PadTile<DPE>;  // the block's V rows: row fragments only
+  using GQ = XorTile<DPE>;  // Q / dO tiles: row and transposed fragments
   constexpr int NVT = kDkdvBlockKeys / 64;  // 64-row V tiles of the block
   __shared__ __attribute__((aligned(16))) bf16 Vb[NVT][GV::ELEMS];
   // two Q / dO buffers; before the loop they hold the block's K rows (as
@@ -904,18 +911,48 @@ __global__ __launch_bounds__(64 * kDkWaves, 1) void dkdv_kernel(BwdParams p) {
   const float c2 = p.scale * kLog2e;
 
 
-  f32x16 dk[DBLK], dv[DBLK];
+  f32x16 dk[DBF], dv[DBF];
 #pragma unroll
-  for (int i = 0; i < DBLK; ++i) {
+  for (int i = 0; i < DBF; ++i) {
     dk[i] = zero16();
     dv[i] = zero16();
   }
+  // the 16-wide tail (kTail): keys 16 t .. 16 t + 15 of the wave's 32, d 64-79,
+  // 16 x 16 C layout (column d = 64 + lane % 16, rows 4 (lane / 16) .. + 3)
+  f32x4 dkt[2], dvt[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) dkt[t] = dvt[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   if (kblk0 < len) {  // block has at least one valid key (block-uniform)
-    XorLanes<DP, KSTEPS> lo;
+    XorLanes<DPE, KSTEPS> lo;
     lo.init_rows_lean(lane);
     lo.init_tr_lean(lane);
-    PadRows<DP> vlo;
+    // transposed tail fragments (B operands of the 16 x 16 x 32 MFMAs): lane
+    // group G = lane / 16 takes queries 16 (1 - G % 2) + 4 (G / 2) + {0..3,
+    // 8..11} of a 32-query half, the order in which v_permlane16_swap leaves
+    // the P / dS A operands, column d = 64 + lane % 16 (lane j of a group
+    // addresses row j / 4, the 8 bytes at column 64 + 4 (j % 4))
+    int tail_off[2];
+    if constexpr (kTail) {
+      const int G = lane >> 4, j = lane & 15;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int row = 16 * (1 - (G & 1)) + 8 * hh + 4 * (G >> 1) + (j >> 2);
+        tail_off[hh] = row * GQ::W + (((8 + ((j & 3) >> 1)) ^ swz(row)) << 3) + 4 * (j & 1);
+      }
+    }
+    auto tail_frag = [&](const bf16* t, int qb) {
+      const bf16x4 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(t + qb * 32 * GQ::W + tail_off[0]));
+      const bf16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(t + qb * 32 * GQ::W + tail_off[1]));
+      bf16x8 r;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        r[i] = lo4[i];
+        r[i + 4] = hi4[i];
+      }
+      return r;
+    };
+    PadRows<DPE> vlo;
     vlo.init(lane);
     DirectLoader<GQ, kDkWaves> qld, gld;
     qld.init(p.sqt, p.D, wave, lane);
@@ -1039,17 +1076,30 @@ __global__ __launch_bounds__(64 * kDkWaves, 1) void dkdv_kernel(BwdParams p) {
         if (qb == 0) prio<2>();
         else prio<0>();
         // dV += P^T dO ; dK += dS^T Q (M = keys, N = d, K = the 32 queries of
-        // this half); step s2 = (h2 = s2 / DBLK, db = s2 % DBLK)
-        pipelined<2 * DBLK, 1>(
+        // this half); step s2 = (h2 = s2 / DBF, db = s2 % DBF)
+        pipelined<2 * DBF, 1>(
             [&](int s2) {
-              const int r0 = qb * 32 + (s2 / DBLK) * 16;
-              return Frag2{lo.tr_frag_lean(Gd, r0, s2 % DBLK), lo.tr_frag_lean(Q, r0, s2 % DBLK)};
+              const int r0 = qb * 32 + (s2 / DBF) * 16;
+              return Frag2{lo.tr_frag_lean(Gd, r0, s2 % DBF), lo.tr_frag_lean(Q, r0, s2 % DBF)};
             },
             [&](int s2, const Frag2& f) {
-              const int h2 = s2 / DBLK, db = s2 % DBLK;
+              const int h2 = s2 / DBF, db = s2 % DBF;
               dv[db] = mfma32x32x16(pf[h2], f.a, dv[db]);
               dk[db] = mfma32x32x16(dsf[h2], f.b, dk[db]);
             });
+        if constexpr (kTail) {
+          // P / dS as 16 x 16 x 32 A operands (key rows 16 t + lane % 16,
+          // 32 queries): lane l holds key l % 32 with queries c_row(8 h2 + i,
+          // l / 32) in pf[h2]; one swap per dword brings every 16-lane group
+          // the right keys, pf[1] then serving keys 0-15 and pf[0] keys 16-31
+          const bf16x8 gt = tail_frag(Gd, qb), qt = tail_frag(Q, qb);
+          permlane16_swap(pf[1], pf[0]);
+          permlane16_swap(dsf[1], dsf[0]);
+          dvt[0] = mfma16x16x32(pf[1], gt, dvt[0]);
+          dvt[1] = mfma16x16x32(pf[0], gt, dvt[1]);
+          dkt[0] = mfma16x16x32(dsf[1], qt, dkt[0]);
+          dkt[1] = mfma16x16x32(dsf[0], qt, dkt[1]);
+        }
       }
       prio<0>();
       buf ^= 1;
@@ -1060,7 +1110,7 @@ __global__ __launch_bounds__(64 * kDkWaves, 1) void dkdv_kernel(BwdParams p) {
   // keys past the valid length (pads) get zero
   const int64_t base = (int64_t)b * p.sdkb + (int64_t)h * p.sdkh;
   const int lane_e = lane_id_fresh(), g_e = lane_e >> 5;  // as in the forward's epilogue
-  using E = cq_epi::KRows<DP>;
+  using E = cq_epi::KRows<DPE>;
   if constexpr (E::kHalfBytes <= (int)sizeof(QG) && E::kHalfBytes <= (int)sizeof(Vb)) {
     // dK, then dV, staged through LDS (cq_epilogue.h: waves 0-3 in the Q / dO
     // buffers, 4-7 in the V tiles) and stored as contiguous row pieces
@@ -1075,9 +1125,15 @@ __global__ __launch_bounds__(64 * kDkWaves, 1) void dkdv_kernel(BwdParams p) {
     for (int tn = 0; tn < 2; ++tn) {
       const float sc = tn == 0 ? p.scale : 1.f;
 #pragma unroll
-      for (int db = 0; db < DBLK; ++db)
+      for (int db = 0; db < DBF; ++db)
 #pragma unroll
         for (int r = 0; r < 16; ++r) st[E::stage_write(db, r, lane_e)] = (tn == 0 ? dk[db][r] : dv[db][r]) * sc;
+      if constexpr (kTail) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) st[E::stage_write_tail(t, i, lane_e)] = (tn == 0 ? dkt[t][i] : dvt[t][i]) * sc;
+      }
       __syncthreads();
       void* const outp = tn == 0 ? (void*)p.ct.dk[c] : (void*)p.ct.dv[c];
       if (wide) {
@@ -1085,9 +1141,11 @@ __global__ __launch_bounds__(64 * kDkWaves, 1) void dkdv_kernel(BwdParams p) {
         for (int it0 = 0; it0 < E::kIters; it0 += 4) {
           f32x4 x[4];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) x[j] = *(const f32x4*)(st + E::stage_read(it0 + j, lane_e));
+          for (int j = 0; j < 4; ++j)
+            if (it0 + j < E::kIters) x[j] = *(const f32x4*)(st + E::stage_read(it0 + j, lane_e));
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
+            if (it0 + j >= E::kIters) break;  // a last group of fewer than four (16-wide d tail)
             const int kk = key0 + E::read_row(it0 + j, lane_e), ch = E::read_chunk(it0 + j, lane_e);
             if (kk >= rows_c || 4 * ch >= p.D) continue;
             const f32x4 y = kk < len ? x[j] : f32x4{0.f, 0.f, 0.f, 0.f};
@@ -1113,25 +1171,26 @@ __global__ __launch_bounds__(64 * kDkWaves, 1) void dkdv_kernel(BwdParams p) {
       }
       __syncthreads();  // the staging rows are rewritten with dV
     }
-    return;
-  }
+  } else {
+    static_assert(!kTail, "the tail variant always fits the staged epilogue");
 #pragma unroll
-  for (int db = 0; db < DBLK; ++db) {
-    const int d = db * 32 + (lane_e & 31);
-    if (d >= p.D) continue;
+    for (int db = 0; db < DBLK; ++db) {
+      const int d = db * 32 + (lane_e & 31);
+      if (d >= p.D) continue;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int kk = key0 + c_row(r, g_e);
-      if (kk >= p.ct_rows[c]) continue;
-      const int64_t e = base + (int64_t)kk * p.sdkt + d;
-      const bool valid = kk < len;
-      const float vk = valid ? dk[db][r] * p.scale : 0.f, vv = valid ? dv[db][r] : 0.f;
-      if (p.dkv_f32) {
-        ((float*)p.ct.dk[c])[e] = vk;
-        ((float*)p.ct.dv[c])[e] = vv;
-      } else {
-        p.ct.dk[c][e] = (bf16)vk;
-        p.ct.dv[c][e] = (bf16)vv;
+      for (int r = 0; r < 16; ++r) {
+        const int kk = key0 + c_row(r, g_e);
+        if (kk >= p.ct_rows[c]) continue;
+        const int64_t e = base + (int64_t)kk * p.sdkt + d;
+        const bool valid = kk < len;
+        const float vk = valid ? dk[db][r] * p.scale : 0.f, vv = valid ? dv[db][r] : 0.f;
+        if (p.dkv_f32) {
+          ((float*)p.ct.dk[c])[e] = vk;
+          ((float*)p.ct.dv[c])[e] = vv;
+        } else {
+          p.ct.dk[c][e] = (bf16)vk;
+          p.ct.dv[c][e] = (bf16)vv;
+        }
       }
     }
   }

@@ -12,7 +12,9 @@
 //   * every global store lies inside the caller's allocation, no output
 //     element is written twice over the grid, and every element of every
 //     output row (d < D) is written;
-// and counts the 4-element stores whose address is not 8-byte aligned.
+// and counts the 4-element stores whose address is not 8-byte aligned.  DP 80
+// is dK / dV's layout at head dims 72 / 80: two 32-wide d blocks and a
+// 16-wide last one staged from the 16 x 16 accumulator layout.
 //
 // usage: cq_epilogue_bounds kind DP D B H rows n_split elem_bytes wide
 //        half0_bytes half1_bytes view_offset stride_b stride_h stride_t
@@ -38,7 +40,7 @@ struct Counts {
 template <class E, int DP, bool Q>
 void walk_block(Counts& n, int wave_rows0, int valid_rows, int D, int eb, bool wide, const long long half_bytes[2],
                 long long base, long long st, long long alloc, std::vector<unsigned char>& hit) {
-  constexpr int DBLK = DP / 32;
+  constexpr int DBLK = DP / 32;  // 32-wide d blocks; DP % 32 == 16: a 16-wide last one (dK / dV)
   for (int wave = 0; wave < cq_epi::kWaves; ++wave) {
     const long long lim = half_bytes[cq_epi::half(wave)];
     std::vector<int> wr(cq_epi::kRows * E::kSR, 0), rd(wr.size(), 0);
@@ -56,6 +58,18 @@ void walk_block(Counts& n, int wave_rows0, int valid_rows, int D, int eb, bool w
           }
           for (int e = 0; e < len; ++e) ++wr[x + e];
         }
+    if constexpr (!Q && DP % 32 == 16) {
+      for (int lane = 0; lane < 64; ++lane)
+        for (int t = 0; t < 2; ++t)
+          for (int i = 0; i < 4; ++i) {
+            const int x = E::stage_write_tail(t, i, lane);
+            if (!in_lds(x, 1)) {
+              ++n.lds_oob;
+              continue;
+            }
+            ++wr[x];
+          }
+    }
     const int first_row = wave_rows0 + wave * cq_epi::kRows;
     auto store = [&](int row, int col, int len) {
       const int rr = first_row + row;
@@ -173,7 +187,10 @@ int main(int argc, char** argv) {
     case 32: run<32>(kind, D, B, H, rows, n_split, eb, wide, half_bytes, off, sb, sh, st, split, alloc, chunk_rows, n); break;
     case 64: run<64>(kind, D, B, H, rows, n_split, eb, wide, half_bytes, off, sb, sh, st, split, alloc, chunk_rows, n); break;
     case 96: run<96>(kind, D, B, H, rows, n_split, eb, wide, half_bytes, off, sb, sh, st, split, alloc, chunk_rows, n); break;
-    default: std::fprintf(stderr, "DP must be 32, 64 or 96\n"); return 2;
+    case 80:  // dK / dV with the 16-wide tail
+      if (kind != 'k') { std::fprintf(stderr, "DP 80 is the dK / dV tail layout\n"); return 2; }
+      run<80>(kind, D, B, H, rows, n_split, eb, wide, half_bytes, off, sb, sh, st, split, alloc, chunk_rows, n); break;
+    default: std::fprintf(stderr, "DP must be 32, 64, 80 or 96\n"); return 2;
   }
   std::printf(
       "lds_oob=%lld stage_pad=%lld stage_twice=%lld stage_missing=%lld read_twice=%lld read_unwritten=%lld "

@@ -26,7 +26,7 @@ QKV_TILES = 2 * 2 * 64 * 128 * 2
 
 
 def v_tiles(dp):
-    return 4 * 64 * (dp + 8) * 2
+    return 4 * 64 * (dp + 8) * 2  # at DP 80 (the 16-wide tail) the V tile is PadTile<80>
 
 
 @pytest.fixture(scope="module")
@@ -88,8 +88,9 @@ def test_q_unaligned_bf16_view_takes_the_element_path(walker):
 
 @pytest.mark.parametrize("DP,D,B,H,chunks", [
     (64, 64, 1, 16, [2048] * 4),        # config 2
-    (96, 72, 2, 16, [4096, 4096]),      # config 3 (two of its eight chunks)
-    (96, 80, 1, 2, [300, 97, 1, 256]),  # ragged chunk lengths
+    (80, 72, 2, 16, [4096, 4096]),      # config 3 (two of its eight chunks): the 16-wide d tail
+    (80, 80, 1, 2, [300, 97, 1, 256]),  # ragged chunk lengths
+    (96, 88, 1, 2, [300, 97, 1, 256]),
     (32, 32, 2, 3, [520]),
 ])
 @pytest.mark.parametrize("eb", [2, 4])
