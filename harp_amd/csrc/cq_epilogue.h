@@ -58,6 +58,12 @@ struct QRows : Rows<DP, DP + 4> {
   HARP_HD static int stage_write(int db, int i, int lane) {
     return (lane & 31) * (DP + 4) + db * 32 + c_row(4 * i, lane >> 5);
   }
+  // a 16-wide last d block (DP = 32 n + 16), 16 x 16 accumulator layout:
+  // the four registers of lane `lane` in tile u are query row 16 u + lane %
+  // 16, elements DP - 16 + 4 (lane / 16) .. + 3, staged by one 16-byte write
+  HARP_HD static int stage_write_tail(int u, int lane) {
+    return (16 * u + (lane & 15)) * (DP + 4) + DP - 16 + 4 * (lane >> 4);
+  }
 };
 
 // dK / dV: lane = d column 32 db + lane % 32, register r = key row

@@ -599,8 +599,13 @@ constexpr int kDqPfA = 1;  // S^T / dP^T fragments issued this many steps ahead
 template <int KSTEPS, int DBLK>
 __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
   constexpr int DP = DBLK * 32;
-  using GK = XorTile<DP>;  // K: row and transposed fragments
-  using GV = XorTile<DP>;  // V: row fragments only
+  // At 5 k-steps (head dims 72 and 80) the last d block of dQ^T is 16 wide:
+  // 16 x 16 x 32 MFMAs over d 64-79, as in dkdv_kernel.
+  constexpr bool kTail = KSTEPS == 5 && DBLK == 3;
+  constexpr int DBF = kTail ? DBLK - 1 : DBLK;  // 32-wide d blocks
+  constexpr int DPE = kTail ? 80 : DP;          // d columns the tiles and outputs hold
+  using GK = XorTile<DPE>;  // K: row and transposed fragments
+  using GV = XorTile<DPE>;  // V: row fragments only
   constexpr int NS = kDqSub, KB = 2 * NS;
   __shared__ __attribute__((aligned(16))) bf16 Ks[2][NS][GK::ELEMS];
   __shared__ __attribute__((aligned(16))) bf16 Vs[2][NS][GV::ELEMS];
@@ -639,19 +644,38 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
   }
   const float lse2 = q_ok ? -st0 * c2 : INFINITY;
   const float dlt = q_ok ? -st1 : 0.f;
-  XorLanes<DP, KSTEPS> klo;
+  XorLanes<DPE, KSTEPS> klo;
   klo.init_rows_lean(lane);
   klo.init_tr_lean(lane);
-  XorLanes<DP, KSTEPS> vlo;
+  XorLanes<DPE, KSTEPS> vlo;
   vlo.init_rows_lean(lane);
   DirectLoader<GK, kDqWaves> kld;
   kld.init(p.skt, p.D, wave, lane);
   DirectLoader<GV, kDqWaves> vld;
   vld.init(p.skt, p.D, wave, lane);
 
-  f32x16 dq[DBLK];
+  f32x16 dq[DBF];
 #pragma unroll
-  for (int i = 0; i < DBLK; ++i) dq[i] = zero16();
+  for (int i = 0; i < DBF; ++i) dq[i] = zero16();
+  // the 16-wide tail (kTail): d 64-79 x queries 16 u .. 16 u + 15 of the
+  // wave's 32, 16 x 16 C layout (column = query, rows d = 64 + 4 (lane / 16) + i)
+  f32x4 dqt[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) dqt[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // K^T tail fragments (A operands of those MFMAs): lane group G = lane / 16
+  // takes keys 16 (1 - G % 2) + 4 (G / 2) + {0..3, 8..11} of a 32-key block,
+  // the order v_permlane16_swap leaves the dS^T B operands in, row d = 64 +
+  // lane % 16 (lane j of a group addresses key row j / 4, the 8 bytes at
+  // column 64 + 4 (j % 4))
+  int tail_off[2] = {0, 0};
+  if constexpr (kTail) {
+    const int G = lane >> 4, j = lane & 15;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const int row = 16 * (1 - (G & 1)) + 8 * hh + 4 * (G >> 1) + (j >> 2);
+      tail_off[hh] = row * GK::W + (((8 + ((j & 3) >> 1)) ^ swz(row)) << 3) + 4 * (j & 1);
+    }
+  }
 
   const int64_t kvo = (int64_t)b * p.skb + (int64_t)h * p.skh;
   auto issue = [&](const KvCursor& t, int bf) {
@@ -754,13 +778,30 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
             }
           });
     };
-    // C(j): dQ^T += K_j^T dS_j^T; step i = (16-key half i / DBLK, d block i % DBLK)
+    // C(j): dQ^T += K_j^T dS_j^T; step i = (16-key half i / DBF, d block i % DBF)
     auto phase_c = [&](auto J) {
       constexpr int j = decltype(J)::value;
       const bf16* K = Ks[buf][j / 2];
-      pipelined<2 * DBLK, 2>(
-          [&](int i) { return klo.tr_frag_lean(K, (j & 1) * 32 + (i / DBLK) * 16, i % DBLK); },
-          [&](int i, const bf16x8& a) { dq[i % DBLK] = mfma32x32x16(a, dsf[j & 1][i / DBLK], dq[i % DBLK]); });
+      pipelined<2 * DBF, 2>(
+          [&](int i) { return klo.tr_frag_lean(K, (j & 1) * 32 + (i / DBF) * 16, i % DBF); },
+          [&](int i, const bf16x8& a) { dq[i % DBF] = mfma32x32x16(a, dsf[j & 1][i / DBF], dq[i % DBF]); });
+      if constexpr (kTail) {
+        // dS^T as 16 x 16 x 32 B operands (query columns 16 u + lane % 16,
+        // 32 keys): one swap per dword, dsf[.][1] then serving queries 0-15
+        // and dsf[.][0] queries 16-31
+        const bf16* kt = K + (j & 1) * 32 * GK::W;
+        const bf16x4 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(kt + tail_off[0]));
+        const bf16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(kt + tail_off[1]));
+        bf16x8 a;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          a[i] = lo4[i];
+          a[i + 4] = hi4[i];
+        }
+        permlane16_swap(dsf[j & 1][1], dsf[j & 1][0]);
+        dqt[0] = mfma16x16x32(a, dsf[j & 1][1], dqt[0]);
+        dqt[1] = mfma16x16x32(a, dsf[j & 1][0], dqt[1]);
+      }
     };
     prio<3>();
     phase_a(Int<0>{}, Int<-1>{});
@@ -788,19 +829,23 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
 
   const int lane_e = lane_id_fresh(), g_e = lane_e >> 5;  // as in the forward's epilogue
   const int qi_e = qt * kDqRows + wave * 32 + (lane_e & 31);
-  using E = cq_epi::QRows<DP>;
+  using E = cq_epi::QRows<DPE>;
   if constexpr (E::kHalfBytes <= (int)sizeof(Ks) && E::kHalfBytes <= (int)sizeof(Vs)) {
     // dQ staged through LDS as in the forward (cq_epilogue.h)
     float* const st = (float*)(cq_epi::half(wave) ? &Vs[0][0][0] : &Ks[0][0][0]) + E::stage_base(wave);
     __syncthreads();  // every wave is done with the loop's K / V tiles
 #pragma unroll
-    for (int db = 0; db < DBLK; ++db)
+    for (int db = 0; db < DBF; ++db)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const f32x4 x = {dq[db][4 * i] * p.scale, dq[db][4 * i + 1] * p.scale, dq[db][4 * i + 2] * p.scale,
                          dq[db][4 * i + 3] * p.scale};
         *(f32x4*)(st + E::stage_write(db, i, lane_e)) = x;
       }
+    if constexpr (kTail) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) *(f32x4*)(st + E::stage_write_tail(u, lane_e)) = dqt[u] * p.scale;
+    }
     __syncthreads();
     const int64_t bh = sp.index * p.split_dq + (int64_t)b * p.sdqb + (int64_t)h * p.sdqh;
     const int q0 = qt * kDqRows + wave * 32;
@@ -808,14 +853,15 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
     // else one element per lane and store
     const bool wide = p.dq_f32 || ((((uintptr_t)p.dq & 7u) == 0) && ((p.sdqb | p.sdqh | p.sdqt) & 3) == 0);
     if (wide) {
-      static_assert(E::kIters % 4 == 0, "read back in whole groups of four");
 #pragma unroll
       for (int it0 = 0; it0 < E::kIters; it0 += 4) {
         f32x4 x[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) x[j] = *(const f32x4*)(st + E::stage_read(it0 + j, lane_e));
+        for (int j = 0; j < 4; ++j)
+          if (it0 + j < E::kIters) x[j] = *(const f32x4*)(st + E::stage_read(it0 + j, lane_e));
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
+          if (it0 + j >= E::kIters) break;  // a last group of fewer than four (16-wide d tail)
           const int qi = q0 + E::read_row(it0 + j, lane_e), ch = E::read_chunk(it0 + j, lane_e);
           if (qi >= p.T || 4 * ch >= p.D) continue;
           const int64_t e = bh + (int64_t)qi * p.sdqt + 4 * ch;
@@ -839,10 +885,11 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
       }
     }
   } else if (qi_e < p.T) {
+    static_assert(!kTail, "the tail variant always fits the staged epilogue");
     char* drow = (char*)p.dq + ((sp.index * p.split_dq + (int64_t)b * p.sdqb + (int64_t)h * p.sdqh +
                                  (int64_t)qi_e * p.sdqt) << (p.dq_f32 ? 2 : 1));
 #pragma unroll
-    for (int db = 0; db < DBLK; ++db)
+    for (int db = 0; db < DBF; ++db)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int d = db * 32 + c_row(r, g_e);

@@ -13,8 +13,8 @@
 //     element is written twice over the grid, and every element of every
 //     output row (d < D) is written;
 // and counts the 4-element stores whose address is not 8-byte aligned.  DP 80
-// is dK / dV's layout at head dims 72 / 80: two 32-wide d blocks and a
-// 16-wide last one staged from the 16 x 16 accumulator layout.
+// is the layout at head dims 72 / 80: two 32-wide d blocks and a 16-wide last
+// one staged from the 16 x 16 accumulator layout.
 //
 // usage: cq_epilogue_bounds kind DP D B H rows n_split elem_bytes wide
 //        half0_bytes half1_bytes view_offset stride_b stride_h stride_t
@@ -58,16 +58,21 @@ void walk_block(Counts& n, int wave_rows0, int valid_rows, int D, int eb, bool w
           }
           for (int e = 0; e < len; ++e) ++wr[x + e];
         }
-    if constexpr (!Q && DP % 32 == 16) {
+    if constexpr (DP % 32 == 16) {  // the 16-wide last d block, 16 x 16 accumulator layout
       for (int lane = 0; lane < 64; ++lane)
         for (int t = 0; t < 2; ++t)
-          for (int i = 0; i < 4; ++i) {
-            const int x = E::stage_write_tail(t, i, lane);
-            if (!in_lds(x, 1)) {
+          for (int i = 0; i < (Q ? 1 : 4); ++i) {
+            int x, len;
+            if constexpr (Q) {
+              x = E::stage_write_tail(t, lane), len = 4;
+            } else {
+              x = E::stage_write_tail(t, i, lane), len = 1;
+            }
+            if (!in_lds(x, len) || (Q && x % 4)) {
               ++n.lds_oob;
               continue;
             }
-            ++wr[x];
+            for (int e = 0; e < len; ++e) ++wr[x + e];
           }
     }
     const int first_row = wave_rows0 + wave * cq_epi::kRows;
@@ -187,8 +192,7 @@ int main(int argc, char** argv) {
     case 32: run<32>(kind, D, B, H, rows, n_split, eb, wide, half_bytes, off, sb, sh, st, split, alloc, chunk_rows, n); break;
     case 64: run<64>(kind, D, B, H, rows, n_split, eb, wide, half_bytes, off, sb, sh, st, split, alloc, chunk_rows, n); break;
     case 96: run<96>(kind, D, B, H, rows, n_split, eb, wide, half_bytes, off, sb, sh, st, split, alloc, chunk_rows, n); break;
-    case 80:  // dK / dV with the 16-wide tail
-      if (kind != 'k') { std::fprintf(stderr, "DP 80 is the dK / dV tail layout\n"); return 2; }
+    case 80:  // the 16-wide d tail (head dims 72 / 80)
       run<80>(kind, D, B, H, rows, n_split, eb, wide, half_bytes, off, sb, sh, st, split, alloc, chunk_rows, n); break;
     default: std::fprintf(stderr, "DP must be 32, 64, 80 or 96\n"); return 2;
   }

@@ -55,7 +55,8 @@ Q_HALVES = (QKV_TILES, QKV_TILES)
 
 @pytest.mark.parametrize("DP,D,B,H,T,n_split", [
     (64, 64, 1, 16, 2048, 2),   # config 2: the forward's and dQ's fp32 split partials
-    (96, 72, 2, 16, 4096, 1),   # config 3
+    (80, 72, 2, 16, 4096, 1),   # config 3: the 16-wide d tail
+    (80, 80, 1, 3, 77, 3),
     (96, 96, 1, 3, 77, 3),
     (32, 24, 2, 2, 300, 1),
 ])
@@ -68,10 +69,10 @@ def test_q_fp32_head_major_and_splits(walker, DP, D, B, H, T, n_split):
 
 @pytest.mark.parametrize("eb", [4, 2])
 def test_q_token_major_config3(walker, eb):
-    """O (fp32) and dQ (bf16) of config 3 in the operators' token-major
-    layout: 8-byte aligned 4-element stores."""
+    """dQ (bf16 and fp32) of config 3 in the operators' token-major
+    layout, 16-wide d tail: 8-byte aligned 4-element stores."""
     B, H, T, D = 2, 16, 4096, 72
-    r = walk(walker, "q", 96, D, B, H, T, 1, eb, True, Q_HALVES, 0, T * H * D, D, H * D, 0, B * T * H * D)
+    r = walk(walker, "q", 80, D, B, H, T, 1, eb, True, Q_HALVES, 0, T * H * D, D, H * D, 0, B * T * H * D)
     _clean(r)
     assert r["misaligned"] == 0
 
