@@ -306,8 +306,13 @@ constexpr int kFwdSub = 2;
 template <int KSTEPS, int DBLK>
 __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
   constexpr int DP = DBLK * 32;
-  using GK = XorTile<DP>;  // K: row fragments only
-  using GV = XorTile<DP>;  // V: transposed fragments
+  // At 5 k-steps (head dims 72 and 80) the last d block of O^T is 16 wide:
+  // 16 x 16 x 32 MFMAs over d 64-79, as in dkdv_kernel and dq_kernel.
+  constexpr bool kTail = KSTEPS == 5 && DBLK == 3;
+  constexpr int DBF = kTail ? DBLK - 1 : DBLK;  // 32-wide d blocks
+  constexpr int DPE = kTail ? 80 : DP;          // d columns the tiles and outputs hold
+  using GK = XorTile<DPE>;  // K: row fragments only
+  using GV = XorTile<DPE>;  // V: transposed fragments
   constexpr float kTauExp = 256.f;  // lazy-rescale threshold: a lane's tile sum of P above 2^8
   constexpr int NS = kFwdSub, KB = 2 * NS;  // 64-row sub-tiles, 32-key blocks per tile
   __shared__ __attribute__((aligned(16))) bf16 Ks[2][NS][GK::ELEMS];
@@ -332,18 +337,38 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
       qf[ks] = (q_ok && d0 < p.D) ? *(const bf16x8*)(qrow + d0) : zero8();
     }
   }
-  XorLanes<DP, KSTEPS> klo;
+  XorLanes<DPE, KSTEPS> klo;
   klo.init_rows_lean(lane);
-  XorLanes<DP, KSTEPS> vlo;
+  XorLanes<DPE, KSTEPS> vlo;
   vlo.init(lane, false);
+  // V^T tail fragments (A operands of the tail MFMAs): lane group G = lane /
+  // 16 takes keys 16 (1 - G % 2) + 4 (G / 2) + {0..3, 8..11} of a 32-key
+  // block, the order v_permlane16_swap leaves the P^T B operands in, row d =
+  // 64 + lane % 16 (as dq_kernel's K^T tail)
+  int tail_off[2] = {0, 0};
+  if constexpr (kTail) {
+    const int G = lane >> 4, j = lane & 15;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const int row = 16 * (1 - (G & 1)) + 8 * hh + 4 * (G >> 1) + (j >> 2);
+      tail_off[hh] = row * GV::W + (((8 + ((j & 3) >> 1)) ^ swz(row)) << 3) + 4 * (j & 1);
+    }
+  }
   DirectLoader<GK, kFwdWaves> kld;
   kld.init(p.skt, p.D, wave, lane);
   DirectLoader<GV, kFwdWaves> vld;
   vld.init(p.skt, p.D, wave, lane);
 
-  f32x16 o[DBLK];
+  f32x16 o[DBF];
 #pragma unroll
-  for (int i = 0; i < DBLK; ++i) o[i] = zero16();
+  for (int i = 0; i < DBF; ++i) o[i] = zero16();
+  // the 16-wide tail (kTail): d 64-79 x queries 16 u .. 16 u + 15 of the
+  // wave's 32, 16 x 16 C layout (column = query 16 u + lane % 16, rows d =
+  // 64 + 4 (lane / 16) + i): a lane's tail values belong to another lane's
+  // query, whose statistics it fetches (__shfl) when it scales them
+  f32x4 ot[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) ot[u] = f32x4{0.f, 0.f, 0.f, 0.f};
   // reference point of P (log2 domain): the first keys of a row overflow
   // their exps against -FLT_MAX, which makes the tile rescale
   float m_ref = -__FLT_MAX__;
@@ -454,19 +479,42 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
       const float corr = fast_exp2(m_ref - m_new);
       l_run *= corr;
 #pragma unroll
-      for (int i = 0; i < DBLK; ++i)
+      for (int i = 0; i < DBF; ++i)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[i][r] *= corr;
+      if constexpr (kTail) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) ot[u] *= __shfl(corr, 16 * u + (lane & 15));
+      }
       m_ref = m_new;
       bs = tile_exps();
     }
     l_run += bs;
 
     prio<1>();
-    // O^T += V^T P^T; step i = (ks2 = i / DBLK, db = i % DBLK), 16 keys per ks2
-    pipelined<2 * KB * DBLK, 2>(
-        [&](int i) { return vlo.tr_frag(Vs[buf][(i / DBLK) / 4], ((i / DBLK) % 4) * 16, i % DBLK); },
-        [&](int i, const bf16x8& a) { o[i % DBLK] = mfma32x32x16(a, pf[i / DBLK], o[i % DBLK]); });
+    // O^T += V^T P^T; step i = (ks2 = i / DBF, db = i % DBF), 16 keys per ks2
+    pipelined<2 * KB * DBF, 2>(
+        [&](int i) { return vlo.tr_frag(Vs[buf][(i / DBF) / 4], ((i / DBF) % 4) * 16, i % DBF); },
+        [&](int i, const bf16x8& a) { o[i % DBF] = mfma32x32x16(a, pf[i / DBF], o[i % DBF]); });
+    if constexpr (kTail) {
+      // per 32-key block: P^T as 16 x 16 x 32 B operands (one swap per
+      // dword: pf[2 kb + 1] then serves queries 0-15, pf[2 kb] 16-31)
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        const bf16* vt = Vs[buf][kb / 2] + (kb & 1) * 32 * GV::W;
+        const bf16x4 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(vt + tail_off[0]));
+        const bf16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(vt + tail_off[1]));
+        bf16x8 a;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          a[i] = lo4[i];
+          a[i + 4] = hi4[i];
+        }
+        permlane16_swap(pf[2 * kb + 1], pf[2 * kb]);
+        ot[0] = mfma16x16x32(a, pf[2 * kb + 1], ot[0]);
+        ot[1] = mfma16x16x32(a, pf[2 * kb], ot[1]);
+      }
+    }
 
     prio<0>();
     buf ^= 1;
@@ -481,7 +529,7 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
   // across the loop for them)
   const int lane_e = lane_id_fresh(), g_e = lane_e >> 5;
   const int qi_e = qt * kFwdRows + wave * 32 + (lane_e & 31);
-  using E = cq_epi::QRows<DP>;
+  using E = cq_epi::QRows<DPE>;
   if constexpr (E::kHalfBytes <= (int)sizeof(Ks) && E::kHalfBytes <= (int)sizeof(Vs)) {
     // O / l staged through LDS (cq_epilogue.h: waves 0-3 in the K tiles,
     // 4-7 in the V tiles), then every query row stored as contiguous
@@ -489,23 +537,29 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
     float* const st = (float*)(cq_epi::half(wave) ? &Vs[0][0][0] : &Ks[0][0][0]) + E::stage_base(wave);
     __syncthreads();  // every wave is done with the loop's K / V tiles
 #pragma unroll
-    for (int db = 0; db < DBLK; ++db)
+    for (int db = 0; db < DBF; ++db)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const f32x4 x = {o[db][4 * i] * inv, o[db][4 * i + 1] * inv, o[db][4 * i + 2] * inv, o[db][4 * i + 3] * inv};
         *(f32x4*)(st + E::stage_write(db, i, lane_e)) = x;
       }
+    if constexpr (kTail) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+        *(f32x4*)(st + E::stage_write_tail(u, lane_e)) = ot[u] * __shfl(inv, 16 * u + (lane_e & 15));
+    }
     __syncthreads();
     float* const ob = p.out + sp.index * p.split_o + (int64_t)b * p.sob + (int64_t)h * p.soh;
     const int q0 = qt * kFwdRows + wave * 32;
-    static_assert(E::kIters % 4 == 0, "read back in whole groups of four");
 #pragma unroll
     for (int it0 = 0; it0 < E::kIters; it0 += 4) {
       f32x4 x[4];  // four chunks read back before any is stored: one LDS latency
 #pragma unroll
-      for (int j = 0; j < 4; ++j) x[j] = *(const f32x4*)(st + E::stage_read(it0 + j, lane_e));
+      for (int j = 0; j < 4; ++j)
+        if (it0 + j < E::kIters) x[j] = *(const f32x4*)(st + E::stage_read(it0 + j, lane_e));
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
+        if (it0 + j >= E::kIters) break;  // a last group of fewer than four (16-wide d tail)
         const int qi = q0 + E::read_row(it0 + j, lane_e), ch = E::read_chunk(it0 + j, lane_e);
         if (qi >= p.T || 4 * ch >= p.D) continue;
         float* const o4 = ob + (int64_t)qi * p.sot + 4 * ch;
@@ -516,9 +570,10 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
       }
     }
   } else if (qi_e < p.T) {
+    static_assert(!kTail, "the tail variant always fits the staged epilogue");
     float* orow = p.out + sp.index * p.split_o + (int64_t)b * p.sob + (int64_t)h * p.soh + (int64_t)qi_e * p.sot;
 #pragma unroll
-    for (int db = 0; db < DBLK; ++db)
+    for (int db = 0; db < DBF; ++db)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int d = db * 32 + c_row(r, g_e);
