@@ -110,13 +110,14 @@ def test_padded_row_dk_dv_views(grad_dtype):
     _views_match(D, (4, 0), grad_dtype, seed=33)
 
 
+@pytest.mark.parametrize("head_dim", [64, 72])  # 72: the 16-wide d tail's staging
 @pytest.mark.parametrize("grad_dtype", [torch.bfloat16, torch.float32])
-def test_unaligned_dk_dv_views_head_dim_64(grad_dtype):
-    """Head dim 64 (the compiled dK/dV kernel, element stores): dK / dV views
-    at an odd element offset with an odd row stride, rows only 2-byte aligned
-    in bf16."""
-    print(f"[dkdv unaligned views D=64 {grad_dtype}]", flush=True)
-    _views_match(64, (1, 1), grad_dtype, seed=34)
+def test_unaligned_dk_dv_views_compiled_kernel(grad_dtype, head_dim):
+    """Head dims 64 and 72 (the compiled dK/dV kernel, element stores): dK /
+    dV views at an odd element offset with an odd row stride, rows only
+    2-byte aligned in bf16."""
+    print(f"[dkdv unaligned views D={head_dim} {grad_dtype}]", flush=True)
+    _views_match(head_dim, (1, 1), grad_dtype, seed=34)
 
 
 @pytest.mark.parametrize("heads", [3, 72])  # 6 query tiles: KV split and merge; 144: the kernel's own stores
