@@ -429,3 +429,13 @@ def test_random_shapes_head_dim_128(case):
     rows and 600-key chunks: many loop slots, every exit, ragged and empty
     chunks in ring order."""
     test_random_shapes(case)
+
+
+@pytest.mark.parametrize("case", _random_cases(n=6, seed=7272, head_dim=72, max_rows=600, max_chunk=600)
+                         + _random_cases(n=6, seed=8080, head_dim=80, max_rows=600, max_chunk=600),
+                         ids=lambda c: f"d{c[4]}r{c[0]}")
+def test_random_shapes_d_tail(case):
+    """The same at D = 72 and 80 (the compiled kernels with their 16-wide d
+    tail; at 80 the tail holds no padding column), with up to 600 query rows
+    and 600-key chunks."""
+    test_random_shapes(case)
