@@ -961,9 +961,10 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
 // Backward dK/dV (KV-stationary, as ring_attn.cpp:2723-2816)
 // ---------------------------------------------------------------------------
 // Block = 8 waves x 32 keys (256 keys; two waves per SIMD, one block per CU).
-// Each wave keeps its 32 K rows as MFMA B operands in registers and reads
-// its V rows from the block's LDS copy; dK, dV accumulate in fp32 VGPRs over
-// every query.  Queries stream in 64-row tiles (Q, dO, per-row statistics)
+// Each wave keeps its 32 K rows (and up to head dim 96 its 32 V rows) as
+// MFMA B operands in registers, read once from the block's LDS copies, and
+// otherwise reads its V rows from the block's LDS copy per query tile; dK,
+// dV accumulate in fp32 VGPRs over every query.  Queries stream in 64-row tiles (Q, dO, per-row statistics)
 // through double-buffered LDS; per 32-query half:
 //   A: S' = Q K^T - LSE2 / c, dP' = dO V^T - D   (C row = query, col = key;
 //      the per-row terms are the accumulators' initial values, read from
@@ -1091,7 +1092,10 @@ __global__ __launch_bounds__(64 * kDkWaves, 1) void dkdv_kernel(BwdParams p) {
     constexpr int kSlotsPerStep = (kDmaSlots + KSTEPS - 1) / KSTEPS;
     rsrc_t nq_rs, ng_rs;
 
-    bf16x8 kf[KSTEPS];
+    // V fragments in registers up to 6 k-steps (head dims <= 96); at 8 the
+    // kernel has no registers left for them and reads them per query tile
+    constexpr bool kVRegs = KSTEPS <= 6;
+    bf16x8 kf[KSTEPS], vf[KSTEPS];
     {
       const int64_t kvo = (int64_t)b * p.skb + (int64_t)h * p.skh;
       DirectLoader<GQ, kDkWaves> kld;
@@ -1107,9 +1111,14 @@ __global__ __launch_bounds__(64 * kDkWaves, 1) void dkdv_kernel(BwdParams p) {
       }
       wait_lds_loads();
       __syncthreads();
-      // this wave's 32 K rows: XorTile wave / 2, 32-row block wave % 2
+      // this wave's 32 K rows: XorTile wave / 2, 32-row block wave % 2;
+      // (kVRegs) its 32 V rows, the B operands of dP' = dO V^T, from the
+      // block's V tile the same way: every query tile reuses them
 #pragma unroll
-      for (int ks = 0; ks < KSTEPS; ++ks) kf[ks] = lo.row_frag_lean(kstage + (wave >> 1) * GQ::ELEMS, wave & 1, ks);
+      for (int ks = 0; ks < KSTEPS; ++ks) {
+        kf[ks] = lo.row_frag_lean(kstage + (wave >> 1) * GQ::ELEMS, wave & 1, ks);
+        if constexpr (kVRegs) vf[ks] = vlo.frag(Vb[wave >> 1], wave & 1, ks);
+      }
       __syncthreads();  // every wave has its K fragments: the staging may be overwritten
     }
     const bf16* Vw = Vb[wave >> 1];
@@ -1150,10 +1159,11 @@ __global__ __launch_bounds__(64 * kDkWaves, 1) void dkdv_kernel(BwdParams p) {
         f32x16 s = init_rows(St[buf][0], qb), dp = init_rows(St[buf][1], qb);
         pipelined<KSTEPS, 1>(
             [&](int ks) {
-              return Frag3{lo.row_frag_lean(Q, qb, ks), lo.row_frag_lean(Gd, qb, ks), vlo.frag(Vw, vrb, ks)};
+              Frag3 f{lo.row_frag_lean(Q, qb, ks), lo.row_frag_lean(Gd, qb, ks), {}};
+              if constexpr (!kVRegs) f.c = vlo.frag(Vw, vrb, ks);
+              return f;
             },
             [&](int ks, const Frag3& f) {
-              const bf16x8 v = f.c;
               s = mfma32x32x16(f.a, kf[ks], s);
               if (qb == 0 && has_next) {
 #pragma unroll
@@ -1164,7 +1174,7 @@ __global__ __launch_bounds__(64 * kDkWaves, 1) void dkdv_kernel(BwdParams p) {
                 }
                 if (ks == KSTEPS - 1) issue_stats(nq0, buf ^ 1);
               }
-              dp = mfma32x32x16(f.b, v, dp);
+              dp = mfma32x32x16(f.b, kVRegs ? vf[ks] : f.c, dp);
             });
         if (qb == 0) prio<3>();
         else prio<1>();
