@@ -106,10 +106,14 @@ int check_out_view(const void* p, const int64_t* s, int B, int H, int rows, int 
 
 // Streamed operands are read through 32-bit buffer offsets: every [rows][D]
 // view the kernels walk (one (b, h) of a chunk, of q or of grad_out) must
-// span less than 2^31 bytes.
+// span less than 2^31 bytes, counted over at least 128 rows: the copies of a
+// 128-row tile form their offsets before the buffer's range check zero-fills
+// the rows past a short view, so those offsets must not wrap either.
 int check_extent(int rows, const int64_t* s, const char* name) {
-  if ((int64_t)rows * s[2] * 2 >= ((int64_t)1 << 31))
-    return fail(HARP_RA_EUNSUPPORTED, "%s: %d rows x row stride %lld elements exceeds the 2 GiB buffer range", name,
+  const int64_t span_rows = rows > 128 ? rows : 128;
+  if (span_rows * s[2] * 2 >= ((int64_t)1 << 31))
+    return fail(HARP_RA_EUNSUPPORTED,
+                "%s: %d rows (at least 128 counted) x row stride %lld elements exceeds the 2 GiB buffer range", name,
                 rows, (long long)s[2]);
   return HARP_RA_OK;
 }

@@ -173,6 +173,14 @@ __device__ __forceinline__ void lds_dma_b32(rsrc_t rs, uint32_t lds, uint32_t vo
 
 // Wait for this thread's direct-to-LDS loads (a barrier then publishes them).
 __device__ __forceinline__ void wait_lds_loads() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// The same but leaving this thread's last N vector-memory loads in flight
+// (they complete in issue order): with three tile buffers, the copies of the
+// tile after the next one stay outstanding while the next one is waited for.
+template <int N>
+__device__ __forceinline__ void wait_lds_loads_but() {
+  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit count");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
 
 // Settle a value loaded from global memory before the main loop.  The
 // direct-to-LDS loads are invisible to the compiler, but they count in the

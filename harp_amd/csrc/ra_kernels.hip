@@ -74,7 +74,13 @@ struct PadTile {
 // instruction i (64 slots) goes to waves round-robin; voff holds each lane's
 // byte offset (relative to the tile's first row) or kOOB for padding slots
 // and columns past D, which the range check turns into zeros.
-template <class G, int NW>
+//
+// Pair (head dims <= 64, G an XorTile<128>): the tile holds 128 rows of at
+// most 64 columns, row R at physical row R % 64 in chunks 8 (R / 64) + 0..7,
+// so that every slot of every copy carries data and 128 rows take the LDS of
+// 64.  Row fragments of rows 64 + x are those of row x at k-step ks + 4, and
+// transposed fragments at d block db + 2.
+template <class G, int NW, bool Pair = false>
 struct DirectLoader {
   static constexpr int kInstTot = G::SLOTS / 64;
   static constexpr int kInst = (kInstTot + NW - 1) / NW;
@@ -87,8 +93,14 @@ struct DirectLoader {
       const int inst = wave + k * NW;
       int r, c;
       G::slot(inst * 64 + lane, r, c);
-      const bool ok = inst < kInstTot && c < G::NCH && c * 8 < D;
-      voff[k] = ok ? (uint32_t)(r * row_stride * 2 + c * 16) : kOOB;
+      if constexpr (Pair) {
+        const int dc = c & 7;  // data chunk of row r + 64 (c / 8)
+        const bool ok = inst < kInstTot && dc * 8 < D;
+        voff[k] = ok ? (uint32_t)((r + 64 * (c >> 3)) * row_stride * 2 + dc * 16) : kOOB;
+      } else {
+        const bool ok = inst < kInstTot && c < G::NCH && c * 8 < D;
+        voff[k] = ok ? (uint32_t)(r * row_stride * 2 + c * 16) : kOOB;
+      }
     }
   }
   // this wave's k-th copy instruction of the tile (k < kInst)
@@ -311,12 +323,20 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
   constexpr bool kTail = KSTEPS == 5 && DBLK == 3;
   constexpr int DBF = kTail ? DBLK - 1 : DBLK;  // 32-wide d blocks
   constexpr int DPE = kTail ? 80 : DP;          // d columns the tiles and outputs hold
-  using GK = XorTile<DPE>;  // K: row fragments only
-  using GV = XorTile<DPE>;  // V: transposed fragments
+  // Head dims <= 64: a tile's 128 K (V) rows share one LDS tile in the
+  // pair layout (DirectLoader), half the LDS and half the copy instructions,
+  // and three buffers let each tile's copies be issued two tiles ahead
+  // instead of one: at these head dims a tile's MFMA work is short against
+  // the copies' memory latency.
+  constexpr bool kPair = DPE <= 64;
+  using GK = XorTile<kPair ? 128 : DPE>;  // K: row fragments only
+  using GV = XorTile<kPair ? 128 : DPE>;  // V: transposed fragments
   constexpr float kTauExp = 256.f;  // lazy-rescale threshold: a lane's tile sum of P above 2^8
-  constexpr int NS = kFwdSub, KB = 2 * NS;  // 64-row sub-tiles, 32-key blocks per tile
-  __shared__ __attribute__((aligned(16))) bf16 Ks[2][NS][GK::ELEMS];
-  __shared__ __attribute__((aligned(16))) bf16 Vs[2][NS][GV::ELEMS];
+  constexpr int TK = 64 * kFwdSub, KB = TK / 32;  // keys and 32-key blocks per tile
+  constexpr int NS = kPair ? 1 : kFwdSub;         // LDS tiles (64 rows, or 128 paired) per buffer
+  constexpr int NB = kPair ? 3 : 2;               // buffers
+  __shared__ __attribute__((aligned(16))) bf16 Ks[NB][NS][GK::ELEMS];
+  __shared__ __attribute__((aligned(16))) bf16 Vs[NB][NS][GV::ELEMS];
 
   // the wave index is wave-uniform; readfirstlane lets the compiler keep it in an SGPR
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -339,7 +359,7 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
   }
   XorLanes<DPE, KSTEPS> klo;
   klo.init_rows_lean(lane);
-  XorLanes<DPE, KSTEPS> vlo;
+  XorLanes<kPair ? 128 : DPE, KSTEPS> vlo;  // paired: d blocks 2-3 address rows 64-127
   vlo.init(lane, false);
   // V^T tail fragments (A operands of the tail MFMAs): lane group G = lane /
   // 16 takes keys 16 (1 - G % 2) + 4 (G / 2) + {0..3, 8..11} of a 32-key
@@ -354,9 +374,13 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
       tail_off[hh] = row * GV::W + (((8 + ((j & 3) >> 1)) ^ swz(row)) << 3) + 4 * (j & 1);
     }
   }
-  DirectLoader<GK, kFwdWaves> kld;
+  using LK = DirectLoader<GK, kFwdWaves, kPair>;
+  using LV = DirectLoader<GV, kFwdWaves, kPair>;
+  static_assert(!kPair || (LK::kInstTot % kFwdWaves == 0 && LV::kInstTot % kFwdWaves == 0),
+                "every wave issues the same number of copies (the paired wait counts them)");
+  LK kld;
   kld.init(p.skt, p.D, wave, lane);
-  DirectLoader<GV, kFwdWaves> vld;
+  LV vld;
   vld.init(p.skt, p.D, wave, lane);
 
   f32x16 o[DBF];
@@ -388,7 +412,7 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
   // after the barrier: a burst fills the texture unit's FIFOs, and a wave
   // stalled on issuing a copy cannot issue MFMAs.  Slot j: sub-tile
   // j / kSlotsPerSub, K copies first, then V copies.
-  constexpr int kSlotsK = DirectLoader<GK, kFwdWaves>::kInst, kSlotsV = DirectLoader<GV, kFwdWaves>::kInst;
+  constexpr int kSlotsK = LK::kInst, kSlotsV = LV::kInst;
   constexpr int kSlotsPerSub = kSlotsK + kSlotsV, kDmaSlots = NS * kSlotsPerSub;
   constexpr int kSSteps = KB * KSTEPS, kSlotStride = kSSteps / kDmaSlots > 0 ? kSSteps / kDmaSlots : 1;
   constexpr int kSlotsPerStep = (kDmaSlots + kSSteps - 1) / kSSteps;
@@ -404,19 +428,29 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
   if (cur.step < sp.end) issue(cur, 0);
 #pragma unroll
   for (int ks = 0; ks < KSTEPS; ++ks) settle(qf[ks]);
+  // kPair: the tile after cur, whose copies are in flight while cur runs
+  KvCursor nx1 = cur;
+  if constexpr (kPair) {
+    nx1 = kv_next(p.ct, kvo, cur, TK, sp.end);
+    if (nx1.step < sp.end) issue(nx1, 1);
+  }
 #pragma unroll 1
   while (cur.step < sp.end) {
     const int kv_left = cur.len - cur.k0;
-    const KvCursor nxt = kv_next(p.ct, kvo, cur, 64 * NS, sp.end);
-    wait_lds_loads();
+    const KvCursor nxt = kPair ? nx1 : kv_next(p.ct, kvo, cur, TK, sp.end);
+    // the tile whose copies this one issues (nxt, or the one after it) and its buffer
+    const KvCursor pre = kPair ? kv_next(p.ct, kvo, nxt, TK, sp.end) : nxt;
+    const int pbuf = kPair ? (buf == 0 ? 2 : buf - 1) : (buf ^ 1);
+    if (kPair && nxt.step < sp.end) wait_lds_loads_but<kDmaSlots>();  // nxt's copies may stay in flight
+    else wait_lds_loads();
     __syncthreads();
-    const bool has_next = nxt.step < sp.end;
+    const bool has_next = pre.step < sp.end;
     if (has_next) {
 #pragma unroll
       for (int sb = 0; sb < NS; ++sb) {
-        const int r0 = nxt.k0 + 64 * sb, rows = nxt.len - r0;
-        nk_rs[sb] = rows_rsrc(nxt.k, p.skt, r0, rows);
-        nv_rs[sb] = rows_rsrc(nxt.v, p.skt, r0, rows);
+        const int r0 = pre.k0 + 64 * sb, rows = pre.len - r0;
+        nk_rs[sb] = rows_rsrc(pre.k, p.skt, r0, rows);
+        nv_rs[sb] = rows_rsrc(pre.v, p.skt, r0, rows);
       }
     }
     prio<3>();
@@ -424,18 +458,23 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
     f32x16 s[KB];
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) s[kb] = zero16();
-    pipelined<KB * KSTEPS, 2>([&](int i) { return klo.row_frag_lean(Ks[buf][(i % KB) / 2], i & 1, i / KB); },
+    pipelined<KB * KSTEPS, 2>([&](int i) {
+                                if constexpr (kPair)  // rows 64-127 at k-steps 4-7 of the paired tile
+                                  return klo.row_frag_lean(Ks[buf][0], i & 1, i / KB + 4 * ((i % KB) / 2));
+                                else
+                                  return klo.row_frag_lean(Ks[buf][(i % KB) / 2], i & 1, i / KB);
+                              },
                               [&](int i, const bf16x8& a) {
                                 s[i % KB] = mfma32x32x16(a, qf[i / KB], s[i % KB]);
                                 if (has_next && i % kSlotStride == 0) {
 #pragma unroll
                                   for (int u = 0; u < kSlotsPerStep; ++u) {
                                     const int j = (i / kSlotStride) * kSlotsPerStep + u;
-                                    if (j < kDmaSlots) dma_slot(j, buf ^ 1);
+                                    if (j < kDmaSlots) dma_slot(j, pbuf);
                                   }
                                 }
                               });
-    if (kv_left < 64 * NS) {  // tail tile of a chunk: mask keys past its valid length
+    if (kv_left < TK) {  // tail tile of a chunk: mask keys past its valid length
       // a side-effecting (empty) asm keeps this a real uniform branch instead
       // of selects that would run on every tile
       asm volatile("");
@@ -494,7 +533,12 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
     prio<1>();
     // O^T += V^T P^T; step i = (ks2 = i / DBF, db = i % DBF), 16 keys per ks2
     pipelined<2 * KB * DBF, 2>(
-        [&](int i) { return vlo.tr_frag(Vs[buf][(i / DBF) / 4], ((i / DBF) % 4) * 16, i % DBF); },
+        [&](int i) {
+          if constexpr (kPair)  // rows 64-127 at d blocks 2-3 of the paired tile
+            return vlo.tr_frag(Vs[buf][0], ((i / DBF) % 4) * 16, i % DBF + 2 * ((i / DBF) / 4));
+          else
+            return vlo.tr_frag(Vs[buf][(i / DBF) / 4], ((i / DBF) % 4) * 16, i % DBF);
+        },
         [&](int i, const bf16x8& a) { o[i % DBF] = mfma32x32x16(a, pf[i / DBF], o[i % DBF]); });
     if constexpr (kTail) {
       // per 32-key block: P^T as 16 x 16 x 32 B operands (one swap per
@@ -517,8 +561,9 @@ __global__ __launch_bounds__(64 * kFwdWaves, 1) void fwd_kernel(FwdParams p) {
     }
 
     prio<0>();
-    buf ^= 1;
+    buf = kPair ? (buf == 2 ? 0 : buf + 1) : (buf ^ 1);
     cur = nxt;
+    nx1 = pre;
   }
 
   // m = the reference point (a row without keys: m = -inf, l = 0), l relative to it
@@ -659,11 +704,16 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
   constexpr bool kTail = KSTEPS == 5 && DBLK == 3;
   constexpr int DBF = kTail ? DBLK - 1 : DBLK;  // 32-wide d blocks
   constexpr int DPE = kTail ? 80 : DP;          // d columns the tiles and outputs hold
-  using GK = XorTile<DPE>;  // K: row and transposed fragments
-  using GV = XorTile<DPE>;  // V: row fragments only
-  constexpr int NS = kDqSub, KB = 2 * NS;
-  __shared__ __attribute__((aligned(16))) bf16 Ks[2][NS][GK::ELEMS];
-  __shared__ __attribute__((aligned(16))) bf16 Vs[2][NS][GV::ELEMS];
+  // head dims <= 64: paired K / V tiles, three buffers, copies two tiles
+  // ahead (as in fwd_kernel)
+  constexpr bool kPair = DPE <= 64;
+  using GK = XorTile<kPair ? 128 : DPE>;  // K: row and transposed fragments
+  using GV = XorTile<kPair ? 128 : DPE>;  // V: row fragments only
+  constexpr int TK = 64 * kDqSub, KB = TK / 32;  // keys and 32-key blocks per tile
+  constexpr int NS = kPair ? 1 : kDqSub;         // LDS tiles (64 rows, or 128 paired) per buffer
+  constexpr int NB = kPair ? 3 : 2;              // buffers
+  __shared__ __attribute__((aligned(16))) bf16 Ks[NB][NS][GK::ELEMS];
+  __shared__ __attribute__((aligned(16))) bf16 Vs[NB][NS][GV::ELEMS];
 
   // the wave index is wave-uniform; readfirstlane lets the compiler keep it in an SGPR
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -699,14 +749,18 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
   }
   const float lse2 = q_ok ? -st0 * c2 : INFINITY;
   const float dlt = q_ok ? -st1 : 0.f;
-  XorLanes<DPE, KSTEPS> klo;
+  XorLanes<kPair ? 128 : DPE, KSTEPS> klo;  // paired: d blocks 2-3 address rows 64-127
   klo.init_rows_lean(lane);
   klo.init_tr_lean(lane);
   XorLanes<DPE, KSTEPS> vlo;
   vlo.init_rows_lean(lane);
-  DirectLoader<GK, kDqWaves> kld;
+  using LK = DirectLoader<GK, kDqWaves, kPair>;
+  using LV = DirectLoader<GV, kDqWaves, kPair>;
+  static_assert(!kPair || (LK::kInstTot % kDqWaves == 0 && LV::kInstTot % kDqWaves == 0),
+                "every wave issues the same number of copies (the paired wait counts them)");
+  LK kld;
   kld.init(p.skt, p.D, wave, lane);
-  DirectLoader<GV, kDqWaves> vld;
+  LV vld;
   vld.init(p.skt, p.D, wave, lane);
 
   f32x16 dq[DBF];
@@ -747,7 +801,7 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
   // full for ~1000 cycles, and a wave stalled on issuing a copy cannot issue
   // MFMAs either.  Slot j < kDmaSlots: sub-tile j / kSlotsPerSub, K copies
   // first, then V copies.
-  constexpr int kSlotsK = DirectLoader<GK, kDqWaves>::kInst, kSlotsV = DirectLoader<GV, kDqWaves>::kInst;
+  constexpr int kSlotsK = LK::kInst, kSlotsV = LV::kInst;
   constexpr int kSlotsPerSub = kSlotsK + kSlotsV, kDmaSlots = NS * kSlotsPerSub;
   constexpr int kSlotsPerStep = (kDmaSlots + 2 * KSTEPS - 1) / (2 * KSTEPS);
   rsrc_t nk_rs[NS], nv_rs[NS];
@@ -784,13 +838,23 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
   f32x16 neg_d;
 #pragma unroll
   for (int r = 0; r < 16; ++r) neg_d[r] = kDInit ? -dlt_s : 0.f;
+  // kPair: the tile after cur, whose copies are in flight while cur runs
+  KvCursor nx1 = cur;
+  if constexpr (kPair) {
+    nx1 = kv_next(p.ct, kvo, cur, TK, sp.end);
+    if (nx1.step < sp.end) issue(nx1, 1);
+  }
 #pragma unroll 1
   while (cur.step < sp.end) {
-    const KvCursor nxt = kv_next(p.ct, kvo, cur, 64 * NS, sp.end);
-    wait_lds_loads();
+    const KvCursor nxt = kPair ? nx1 : kv_next(p.ct, kvo, cur, TK, sp.end);
+    // the tile whose copies this one issues (nxt, or the one after it) and its buffer
+    const KvCursor pre = kPair ? kv_next(p.ct, kvo, nxt, TK, sp.end) : nxt;
+    const int pbuf = kPair ? (buf == 0 ? 2 : buf - 1) : (buf ^ 1);
+    if (kPair && nxt.step < sp.end) wait_lds_loads_but<kDmaSlots>();  // nxt's copies may stay in flight
+    else wait_lds_loads();
     __syncthreads();
-    const bool has_next = nxt.step < sp.end;
-    if (has_next) prepare(nxt);
+    const bool has_next = pre.step < sp.end;
+    if (has_next) prepare(pre);
 
     // S^T / dP^T of two 32-key blocks in flight (block j in slot j & 1) and
     // the bf16 dS^T of the block whose dQ product is next
@@ -808,13 +872,15 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
     // A(j), with B(jb) spread over its KSTEPS steps (jb < 0: none)
     auto phase_a = [&](auto J, auto JB) {
       constexpr int j = decltype(J)::value, jb = decltype(JB)::value;
-      const bf16* K = Ks[buf][j / 2];
-      const bf16* V = Vs[buf][j / 2];
+      // paired: block j's rows at k-step offset 4 (j / 2) of the one tile
+      const bf16* K = Ks[buf][kPair ? 0 : j / 2];
+      const bf16* V = Vs[buf][kPair ? 0 : j / 2];
+      constexpr int kso = kPair ? 4 * (j / 2) : 0;
       s[j & 1] = zero16();
       dp[j & 1] = kDInit ? neg_d : zero16();
       constexpr int kRowsPerStep = (16 + KSTEPS - 1) / KSTEPS;
       pipelined<KSTEPS, kDqPfA>(
-          [&](int ks) { return Frag2{klo.row_frag_lean(K, j & 1, ks), vlo.row_frag_lean(V, j & 1, ks)}; },
+          [&](int ks) { return Frag2{klo.row_frag_lean(K, j & 1, ks + kso), vlo.row_frag_lean(V, j & 1, ks + kso)}; },
           [&](int ks, const Frag2& f) {
             s[j & 1] = mfma32x32x16(f.a, qf[ks], s[j & 1]);
             if constexpr (j < 2) {
@@ -822,7 +888,7 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
 #pragma unroll
                 for (int u = 0; u < kSlotsPerStep; ++u) {
                   const int slot = (j * KSTEPS + ks) * kSlotsPerStep + u;
-                  if (slot < kDmaSlots) dma_slot(slot, buf ^ 1);
+                  if (slot < kDmaSlots) dma_slot(slot, pbuf);
                 }
               }
             }
@@ -836,9 +902,10 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
     // C(j): dQ^T += K_j^T dS_j^T; step i = (16-key half i / DBF, d block i % DBF)
     auto phase_c = [&](auto J) {
       constexpr int j = decltype(J)::value;
-      const bf16* K = Ks[buf][j / 2];
+      const bf16* K = Ks[buf][kPair ? 0 : j / 2];
+      constexpr int dbo = kPair ? 2 * (j / 2) : 0;  // paired: block j's rows at d block offset 2 (j / 2)
       pipelined<2 * DBF, 2>(
-          [&](int i) { return klo.tr_frag_lean(K, (j & 1) * 32 + (i / DBF) * 16, i % DBF); },
+          [&](int i) { return klo.tr_frag_lean(K, (j & 1) * 32 + (i / DBF) * 16, i % DBF + dbo); },
           [&](int i, const bf16x8& a) { dq[i % DBF] = mfma32x32x16(a, dsf[j & 1][i / DBF], dq[i % DBF]); });
       if constexpr (kTail) {
         // dS^T as 16 x 16 x 32 B operands (query columns 16 u + lane % 16,
@@ -878,8 +945,9 @@ __global__ __launch_bounds__(64 * kDqWaves, 1) void dq_kernel(BwdParams p) {
     phase_c(Int<KB - 1>{});
     prio<0>();
 
-    buf ^= 1;
+    buf = kPair ? (buf == 2 ? 0 : buf + 1) : (buf ^ 1);
     cur = nxt;
+    nx1 = pre;
   }
 
   const int lane_e = lane_id_fresh(), g_e = lane_e >> 5;  // as in the forward's epilogue

@@ -80,6 +80,9 @@ def _fwd_call(**over):
         # a row stride of 0 (an expanded view) or below D would cut every row short
         (dict(ks=_lib.i64_array([8 * 64 * 128, 64, 0, 1])), _lib.HARP_RA_EINVAL, "row stride"),
         (dict(qs=_lib.i64_array([8 * 64 * 128, 64, 56, 1])), _lib.HARP_RA_EINVAL, "row stride"),
+        # a short chunk whose rows lie 32 MiB apart: a 128-row tile's copy
+        # offsets would pass 2^32 (the extent counts at least 128 rows)
+        (dict(ks=_lib.i64_array([8 * 64 * 128, 64, 1 << 24, 1]), tc=16), _lib.HARP_RA_EUNSUPPORTED, "buffer range"),
         # outputs whose strides alias elements are refused (stores would race)
         (dict(os=_lib.i64_array([8 * 64 * 128, 64, 0, 1])), _lib.HARP_RA_EINVAL, "overlap"),
         (dict(os=_lib.i64_array([8 * 64 * 128, 0, 8 * 64, 1])), _lib.HARP_RA_EINVAL, "overlap"),
