@@ -147,6 +147,7 @@ class Emitter:
             self.nop(far + MFMA_RAW + 1 - self.pos)
 
     def wait_lgkm(self, n):
+        n = min(n, 15)  # the counter's field is 4 bits: waiting for 15 retires more, never fewer
         self.raw(f"s_waitcnt lgkmcnt({n})")
         self.lds = self.lds[len(self.lds) - n:] if n else []
 

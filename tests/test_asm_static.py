@@ -126,3 +126,20 @@ def test_branch_joins_take_the_worst_path():
     ])
     bad = A.check(prog)
     assert any(v.rule == "mfma_raw" and v.have < 12 for v in bad)
+
+
+def test_emitter_lds_waits_fit_the_counter():
+    """The emitter's LDS waits never exceed the 4-bit lgkmcnt field: with 20
+    reads outstanding, a wait that needs 18 left is emitted as 15 (retiring
+    three more than needed), and the tracker keeps the 15 youngest."""
+    import sys
+    from pathlib import Path
+    sys.path.insert(0, str(Path(__file__).resolve().parents[1] / "harp_amd" / "csrc"))
+    import asm_sched
+    em = asm_sched.Emitter()
+    em.lds = [{f"v{i}"} for i in range(20)]
+    em.wait_lgkm(18)
+    assert em.lines[-1] == "s_waitcnt lgkmcnt(15)"
+    assert em.lds == [{f"v{i}"} for i in range(5, 20)]
+    em.wait_lgkm(0)
+    assert em.lines[-1] == "s_waitcnt lgkmcnt(0)" and em.lds == []
